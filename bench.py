@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the MI355X event-memory operator.
+
+Metric: event-memory prefill tokens/sec at 1 GPU + achieved HBM
+GB/s (% of peak).  Workload: BASELINE cfg4, the latest-1 forward of
+causal_last_k_lookup at B=4, T=65536, H=16 heads, A=65536 addresses, D=64 bf16
+payload (N = 4,194,304 records), synthetic seeded inputs resident in HBM.
+
+One "step" is one causal_last_k_lookup call over the whole batch.  `value` is
+B*T tokens per step / measured step time.  Prints one JSON line with:
+  roofline     the dominant kernel (the payload gather), timed with HIP events
+               on its launch stream inside the timed region, against 8 TB/s;
+  op_roofline  the whole operator against the same peak, using the
+               inputs-read-once + outputs-written-once bytes of the call;
+  cpu_baseline the reference algorithm restated on the host CPU (torch),
+               timed on a bounded sample on this box's cores.
+Only one GPU is supported: --gpus N with N > 1 exits with a message.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ravel-lm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "event-memory prefill tokens/sec at 1 GPU + achieved HBM GB/s (% of peak)"
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gather_cfg4_traffic.json")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--adversarial", action="store_true", help="90%% of records at address 0")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(w, budget_s):
+    """Reference algorithm on the host: torch sort / searchsorted / gathers."""
+    import torch
+
+    from oracle import torch_ref
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    write = w.write.cpu()
+    payload = w.payload.cpu()
+    B, T, C, D = w.shape
+    log(f"cpu baseline: {threads} threads, full cfg4 call per sample")
+    torch_ref.latest_k(write, payload, address_space=w.address_space, k=w.k)  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        torch_ref.latest_k(write, payload, address_space=w.address_space, k=w.k)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": B * T / med,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} full cfg4 latest-1 calls (median {med:.3f} s) of the reference's "
+                  "sort/searchsorted/gather algorithm restated with torch on the CPU",
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): the operator shards "
+              "by (batch, head) stream with no communication, so each GPU would run this same "
+              "single-GPU measurement on its share.", flush=True)
+        sys.exit(2)
+
+    import torch
+
+    from ravel_em import _native as nat
+    from ravel_em import causal_last_k_lookup, workloads
+
+    dev = torch.device("cuda", 0)
+    log("generating cfg4 inputs on the device")
+    w = workloads.cfg4(dev, adversarial=args.adversarial)
+    B, T, C, D = w.shape
+    N, k, A = B * T * C, w.k, w.address_space
+    torch.cuda.synchronize()
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            vals, mask = causal_last_k_lookup(w.write, w.payload, w.read, address_space=A, k=k)
+        torch.cuda.synchronize()
+
+        # Timed region A: the drop-in call, as model.py makes it.
+        log(f"timing {args.steps} steps of causal_last_k_lookup")
+        t_begin = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        t_begin.record()
+        for _ in range(args.steps):
+            vals, mask = causal_last_k_lookup(w.write, w.payload, w.read, address_space=A, k=k)
+        t_end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        ms = t_begin.elapsed_time(t_end) / args.steps
+
+        # Timed region B: the same kernels as resolve + gather calls, with HIP
+        # events around the gather on its launch stream (torch's current stream).
+        lib = nat.library()
+        stream = torch.cuda.current_stream(dev)
+        src = torch.empty(B, T, C, k, dtype=torch.int32, device=dev)
+        vals_b = torch.empty_like(vals)
+        mask_b = torch.empty_like(mask)
+        ws = nat.workspace(lib.ravel_em_latest_k_resolve_workspace(B, T, C, A, k, 0, 0), dev)
+        row_bytes = D * w.payload.element_size()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+        b_begin = torch.cuda.Event(enable_timing=True)
+        b_end = torch.cuda.Event(enable_timing=True)
+        b_begin.record()
+        for e0, e1 in ev:
+            nat.check(lib.ravel_em_latest_k_resolve(
+                w.write.data_ptr(), None, nat.INT64, None, B, T, C, A, k, src.data_ptr(),
+                ws.data_ptr(), ws.numel(), stream.cuda_stream))
+            e0.record(stream)
+            nat.check(lib.ravel_em_gather_rows(
+                w.payload.data_ptr(), N, row_bytes, src.data_ptr(), N * k, vals_b.data_ptr(),
+                mask_b.data_ptr(), stream.cuda_stream))
+            e1.record(stream)
+        b_end.record()
+        torch.cuda.synchronize()
+        gather_ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / len(ev)
+        split_ms = b_begin.elapsed_time(b_end) / args.steps
+        assert torch.equal(vals_b, vals) and torch.equal(mask_b, mask), "split path differs from fused call"
+        valid_slots = int(mask.sum().item())
+
+    # Gather kernel bytes: src read (4 B/slot), values + mask written, and one
+    # payload row read per valid slot.
+    gather_bytes = N * k * (4 + 1 + row_bytes) + valid_slots * row_bytes
+    gather_gbps = gather_bytes / (gather_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    op_bytes = workloads.algorithmic_bytes_latest_k(w)
+    op_gbps = op_bytes / (ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": B * T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg4" + ("_adversarial" if args.adversarial else "")
+            + ": causal_last_k_lookup latest-1 forward, B=4 T=65536 H=16 A=65536 D=64 bf16",
+            "B": B, "T": T, "H": C, "A": A, "D": D, "k": k,
+            "records": N, "payload_dtype": "bf16", "sort_key": "u32 (a<<16|t) per (b,h) segment",
+        },
+        "achieved_GBps": op_gbps,
+        "achieved_frac_of_peak": op_gbps / PEAK_HBM_GBPS,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gather_rows_kernel",
+            "achieved": gather_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": gather_gbps / PEAK_HBM_GBPS,
+            "traffic": traffic,
+            "avg_launch_ms": gather_ms,
+            "bytes_per_launch": gather_bytes,
+            "valid_slot_fraction": valid_slots / (N * k),
+        },
+        "op_roofline": {
+            "bound": "hbm",
+            "achieved": op_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": op_gbps / PEAK_HBM_GBPS,
+            "bytes_per_call": op_bytes,
+            "split_path_ms_per_step": split_ms,
+        },
+        "wall_s_timed_region": wall,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,178 @@
+/*
+ * ravel_em.h — C ABI of the MI355X (gfx950) RAVEL event-memory library.
+ *
+ * Drop-in boundary for the reference operator module ravel_lm/ravel_memory.py.
+ * Every entry point:
+ *   - takes raw device pointers of contiguous buffers, sizes and dtype codes
+ *     (no framework types cross the ABI);
+ *   - enqueues its kernels on `stream` (a hipStream_t), never synchronizes,
+ *     never allocates device memory: scratch comes from the caller's
+ *     `workspace`, sized by the matching *_workspace() query;
+ *   - returns RAVEL_EM_OK (0) or an error code, with a message available from
+ *     ravel_em_last_error() (thread-local).  No C++ exception crosses the ABI.
+ *
+ * Shapes follow the reference: B batch, T time, C memory heads, A address
+ * space, D payload width, k latest-k slots, N = B*T*C records (N < 2^31).
+ * Bool outputs are one byte per element (0/1), matching torch.bool storage.
+ */
+#ifndef RAVEL_EM_H
+#define RAVEL_EM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+enum {
+  RAVEL_EM_INT32 = 1,
+  RAVEL_EM_INT64 = 2,
+  RAVEL_EM_FLOAT32 = 10,
+  RAVEL_EM_BFLOAT16 = 11,
+  RAVEL_EM_FLOAT16 = 12,
+  RAVEL_EM_FLOAT64 = 13
+};
+
+/* status codes */
+enum {
+  RAVEL_EM_OK = 0,
+  RAVEL_EM_EINVAL = 1,     /* bad argument (shape, dtype, null pointer, size limit) */
+  RAVEL_EM_EHIP = 2,       /* a HIP launch failed */
+  RAVEL_EM_EWORKSPACE = 3  /* workspace smaller than the *_workspace() query */
+};
+
+/* Message of the last failed call on this thread ("" when none). */
+const char* ravel_em_last_error(void);
+
+/* ABI version (bumped on any signature change). */
+int ravel_em_abi_version(void);
+
+/*
+ * Key width rule of _composite_key_dtype (ravel_lm/ravel_memory.py:45-49):
+ * returns 32 when B*C*A*(T+1) <= 2^31-1, else 64.
+ */
+int ravel_em_key_bits(int64_t B, int64_t T, int64_t C, int64_t A);
+
+/*
+ * Sorted composite keys and permutation, i.e. `torch.sort(flat_keys)` of
+ * ravel_lm/ravel_memory.py:126-151 (keys ((b*C+c)*A+a)*(T+1)+t, masked times
+ * removed).  Writes the first n_valid = C * (number of true write_mask entries)
+ * elements (N when write_mask is NULL) of out_sorted_keys (int32 when
+ * ravel_em_key_bits() == 32, else int64) and out_order (int64 indices into the
+ * mask-compacted flat tape).
+ */
+size_t ravel_em_sort_order_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int has_mask);
+int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* write_mask,
+                        int64_t B, int64_t T, int64_t C, int64_t A, void* out_sorted_keys,
+                        int64_t* out_order, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * causal_last_k_lookup forward (ravel_lm/ravel_memory.py:52-176).
+ *   write_addr, read_addr [B,T,C] int32/int64 (read_addr NULL = write_addr),
+ *   write_mask [B,T] bool or NULL, payload [B,T,C,D].
+ *   out_values [B,T,C,k,D] (payload dtype), out_mask [B,T,C,k] bool,
+ *   out_src [B,T,C,k] int32 source record index or -1 (NULL = not wanted).
+ * Missing slots are +0.0.
+ */
+size_t ravel_em_latest_k_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
+                                   int has_read, int has_mask, int want_src);
+int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                          const uint8_t* write_mask, const void* payload, int payload_dtype,
+                          int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, int64_t k,
+                          void* out_values, uint8_t* out_mask, int32_t* out_src, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * The two stages of ravel_em_latest_k_fwd as separate calls, for callers that
+ * gather several payload tensors through one resolution or time the stages:
+ *   resolve: out_src [B,T,C,k] int32 source record index or -1
+ *            (the sort + searchsorted + stream check, ravel_memory.py:126-168);
+ *   gather:  out_values[r] = rows[src[r]] (zeros when src[r] < 0) and
+ *            out_mask[r] = src[r] >= 0 for n_rows rows of row_bytes bytes, rows
+ *            holding n_src rows (the index_select of ravel_memory.py:173-175).
+ */
+size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
+                                           int has_read, int has_mask);
+int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int addr_dtype,
+                              const uint8_t* write_mask, int64_t B, int64_t T, int64_t C,
+                              int64_t A, int64_t k, int32_t* out_src, void* workspace,
+                              size_t workspace_bytes, void* stream);
+int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, const int32_t* src,
+                         int64_t n_rows, void* out_values, uint8_t* out_mask, void* stream);
+
+/*
+ * Backward of causal_last_k_lookup (autograd of ravel_memory.py:173-175;
+ * GPU arm triton_latest1.py:132-142): grad_payload[src] += grad_values.
+ * `chain` = 1 selects the deterministic successor-chain kernel, valid only when
+ * the forward had read == write and no write_mask.
+ */
+size_t ravel_em_latest_k_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k,
+                                       int payload_dtype, int chain);
+int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int payload_dtype,
+                          int64_t B, int64_t T, int64_t C, int64_t D, int64_t k, int chain,
+                          void* grad_payload, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * causal_sum_lookup forward (ravel_lm/ravel_memory.py:179-241).
+ *   out_sum [B,T,C,D] (payload dtype), out_mask [B,T,C] bool.
+ */
+size_t ravel_em_seg_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                  int has_read, int has_mask, int payload_dtype);
+int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                         const uint8_t* write_mask, const void* payload, int payload_dtype,
+                         int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, void* out_sum,
+                         uint8_t* out_mask, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* Backward of causal_sum_lookup (autograd of the cumsum path, ravel_memory.py:216-241). */
+size_t ravel_em_seg_sum_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                      int has_read, int has_mask, int payload_dtype);
+int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                         const uint8_t* write_mask, const void* grad_sum, int payload_dtype,
+                         int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                         void* grad_payload, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
+ * Decode cache, RavelLayerCache (ravel_lm/ravel_memory.py:244-292) with k slots:
+ *   values [B,C,A,k,D] (payload dtype), filled [B,C,A,k] bool; k = 1 is the
+ *   reference's [B,C,A,D] / [B,C,A] layout.  Addresses [B,C] are clamped to
+ *   [0, A-1].
+ * read  (ravel_memory.py:271-281): out_values [B,C,k,D], out_mask [B,C,k].
+ * write (ravel_memory.py:283-292): shift-insert payload [B,C,D] at slot 0.
+ * step: read at read_addr, then write at write_addr, in one launch
+ *   (RavelMemoryLayer.step order, ravel_lm/model.py:421-424).
+ */
+int ravel_em_cache_read(const void* values, const uint8_t* filled, const void* addr,
+                        int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,
+                        int64_t k, int64_t D, void* out_values, uint8_t* out_mask, void* stream);
+int ravel_em_cache_write(void* values, uint8_t* filled, const void* addr, int addr_dtype,
+                         const void* payload, int payload_dtype, int64_t B, int64_t C, int64_t A,
+                         int64_t k, int64_t D, void* stream);
+int ravel_em_cache_step(void* values, uint8_t* filled, const void* read_addr,
+                        const void* write_addr, int addr_dtype, const void* payload,
+                        int payload_dtype, int64_t B, int64_t C, int64_t A, int64_t k, int64_t D,
+                        void* out_values, uint8_t* out_mask, void* stream);
+
+/*
+ * Build the decode cache of a whole prefix in one pass: the state that T
+ * successive cache writes of write_addr[:, t] / payload[:, t] leave behind
+ * (the reference prefills token by token, ravel_lm/model.py:600-602).
+ * write_addr [B,T,C] (clamped), write_mask [B,T] or NULL, payload [B,T,C,D].
+ */
+size_t ravel_em_cache_prefill_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int has_mask);
+int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t* write_mask,
+                           const void* payload, int payload_dtype, int64_t B, int64_t T,
+                           int64_t C, int64_t D, int64_t A, int64_t k, void* values,
+                           uint8_t* filled, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAVEL_EM_H */

@@ -1,0 +1,164 @@
+"""CPU oracle of the RAVEL event-memory operator.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this package, and only as the checker (or, for
+the baseline, as the thing timed on the host): the product path in
+ravel-lm_amd/ravel_em never touches it.
+
+Three independent restatements of the reference operator
+(ravel_lm/ravel_memory.py):
+  * ravel_oracle.c (wrapped here): per-stream history replay in plain C,
+    sized for full BASELINE shapes;
+  * torch_ref.py: the reference's own algorithm (composite keys, torch.sort,
+    searchsorted, gathers, global cumsum) restated on the CPU; it is also the
+    CPU baseline timed by bench.py;
+  * brute.py: pure-Python dictionaries for tiny inputs.
+
+Pinning (what each function is checked against) is listed in tests/ and in the
+module docstrings; every function here has at least one check that a
+plausible mistake fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "ravel_oracle.c")
+LIB_PATH = os.path.join(HERE, "libravel_oracle.so")
+
+_vp, _i64 = ctypes.c_void_p, ctypes.c_int64
+_SIGS = {
+    "oracle_key_bits": (ctypes.c_int, [_i64, _i64, _i64, _i64]),
+    "oracle_sort_order": (_i64, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "oracle_latest_k": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "oracle_seg_sum": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "oracle_cache_prefill": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+}
+_lib = None
+
+
+def build() -> str:
+    """Compile the C restatement with gcc into oracle/libravel_oracle.so."""
+    tmp = LIB_PATH + ".tmp"
+    subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-o", tmp, SRC], check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _np_i64(t) -> np.ndarray:
+    if isinstance(t, torch.Tensor):
+        t = t.detach().cpu().to(torch.int64).numpy()
+    return np.ascontiguousarray(t, dtype=np.int64)
+
+
+def _np_mask(m) -> Optional[np.ndarray]:
+    if m is None:
+        return None
+    if isinstance(m, torch.Tensor):
+        m = m.detach().cpu().bool().numpy()
+    return np.ascontiguousarray(m, dtype=np.uint8)
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+def key_bits(B: int, T: int, C: int, A: int) -> int:
+    return lib().oracle_key_bits(B, T, C, A)
+
+
+def sort_order(write, *, address_space: int, write_mask=None) -> Tuple[np.ndarray, np.ndarray]:
+    """(sorted composite keys, order) of ravel_memory.py:133-151 (int64 both)."""
+    w = _np_i64(write)
+    B, T, C = w.shape
+    m = _np_mask(write_mask)
+    N = B * T * C
+    keys = np.empty(max(N, 1), dtype=np.int64)
+    order = np.empty(max(N, 1), dtype=np.int64)
+    n = lib().oracle_sort_order(_p(w), _p(m), B, T, C, address_space, _p(keys), _p(order))
+    return keys[:n], order[:n]
+
+
+def latest_k_src(write, read=None, *, address_space: int, k: int = 1, write_mask=None) -> np.ndarray:
+    """Source record index (or -1) of every latest-k slot, [B,T,C,k] int32."""
+    w = _np_i64(write)
+    r = None if read is None else _np_i64(read)
+    B, T, C = w.shape
+    m = _np_mask(write_mask)
+    src = np.empty((B, T, C, k), dtype=np.int32)
+    rc = lib().oracle_latest_k(_p(w), _p(r), _p(m), B, T, C, address_space, k, _p(src))
+    assert rc == 0
+    return src
+
+
+def gather_slots(payload: torch.Tensor, src: np.ndarray) -> Tuple[torch.Tensor, torch.Tensor]:
+    """values[b,t,c,j] = payload row src (zeros where src < 0), plus the mask."""
+    B, T, C, D = payload.shape
+    flat = payload.detach().cpu().reshape(-1, D)
+    s = torch.from_numpy(src.astype(np.int64)).reshape(-1)
+    valid = s >= 0
+    vals = flat.index_select(0, s.clamp_min(0))
+    vals = torch.where(valid.view(-1, 1), vals, torch.zeros((), dtype=vals.dtype))
+    k = src.shape[-1]
+    return vals.view(B, T, C, k, D), valid.view(B, T, C, k)
+
+
+def latest_k(write, payload, read=None, *, address_space: int, k: int = 1, write_mask=None):
+    """Oracle of causal_last_k_lookup: (values, mask, src) on the CPU."""
+    src = latest_k_src(write, read, address_space=address_space, k=k, write_mask=write_mask)
+    vals, mask = gather_slots(payload, src)
+    return vals, mask, src
+
+
+def seg_sum(write, payload, read=None, *, address_space: int, write_mask=None):
+    """Oracle of causal_sum_lookup in fp64: (sum float64 [B,T,C,D], mask bool)."""
+    w = _np_i64(write)
+    r = None if read is None else _np_i64(read)
+    B, T, C = w.shape
+    D = payload.shape[-1]
+    m = _np_mask(write_mask)
+    p = np.ascontiguousarray(payload.detach().cpu().double().numpy())
+    out = np.empty((B, T, C, D), dtype=np.float64)
+    mask = np.empty((B, T, C), dtype=np.uint8)
+    rc = lib().oracle_seg_sum(_p(w), _p(r), _p(m), _p(p), B, T, C, address_space, D, _p(out), _p(mask))
+    assert rc == 0
+    return torch.from_numpy(out), torch.from_numpy(mask.astype(bool))
+
+
+def cache_prefill(write, payload, *, address_space: int, k: int, write_mask=None):
+    """Oracle of T sequential cache writes: (values [B,C,A,k,D], filled [B,C,A,k])."""
+    w = _np_i64(write)
+    B, T, C = w.shape
+    D = payload.shape[-1]
+    pc = payload.detach().cpu().contiguous()
+    esz = pc.element_size()
+    raw = pc.view(torch.uint8).numpy() if esz > 1 else pc.numpy()
+    raw = np.ascontiguousarray(raw)
+    m = _np_mask(write_mask)
+    A = address_space
+    values = np.zeros(B * C * A * k * D * esz, dtype=np.uint8)
+    filled = np.zeros(B * C * A * k, dtype=np.uint8)
+    rc = lib().oracle_cache_prefill(_p(w), _p(m), _p(raw), B, T, C, A, k, D * esz, _p(values), _p(filled))
+    assert rc == 0
+    vals = torch.from_numpy(values).view(pc.dtype).view(B, C, A, k, D)
+    return vals, torch.from_numpy(filled.astype(bool)).view(B, C, A, k)

@@ -1,0 +1,603 @@
+// extern "C" entry points of the event-memory library (declared in
+// include/ravel_em.h).  Host code only: argument checks, workspace planning and
+// the kernel sequence of each operator.
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ravel_em.h"
+#include "em_common.h"
+
+namespace rem {
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(RAVEL_EM_EHIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+// Bump allocator over the caller's workspace; with base == nullptr it only
+// measures.
+struct Bump {
+  char* base;
+  size_t off = 0;
+  explicit Bump(void* b) : base((char*)b) {}
+  template <typename X>
+  X* take(size_t n) {
+    off = (off + 255) & ~(size_t)255;
+    X* p = base ? (X*)(base + off) : nullptr;
+    off += n * sizeof(X);
+    return p;
+  }
+};
+
+constexpr int64_t kMaxRecords = (int64_t)0x7fffffff;
+
+bool mul_ok(int64_t a, int64_t b, int64_t* out) {
+  __int128 r = (__int128)a * b;
+  if (r > (__int128)INT64_MAX) return false;
+  *out = (int64_t)r;
+  return true;
+}
+
+int check_tape(int64_t B, int64_t T, int64_t C, int64_t A) {
+  if (B < 0 || T < 0 || C < 0) return fail(RAVEL_EM_EINVAL, "negative shape B=%lld T=%lld C=%lld", (long long)B, (long long)T, (long long)C);
+  if (A < 1) return fail(RAVEL_EM_EINVAL, "address_space must be >= 1, got %lld", (long long)A);
+  int64_t bt, n;
+  if (!mul_ok(B, T, &bt) || !mul_ok(bt, C, &n) || n > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "B*T*C must be < 2^31 records");
+  if (A > ((int64_t)1 << 40)) return fail(RAVEL_EM_EINVAL, "address_space must be <= 2^40");
+  return RAVEL_EM_OK;
+}
+
+int check_addr_dtype(int dt) {
+  if (dt != kI32 && dt != kI64) return fail(RAVEL_EM_EINVAL, "address dtype must be int32 or int64 (code %d)", dt);
+  return RAVEL_EM_OK;
+}
+
+int check_payload_dtype(int dt) {
+  if (dt != kF32 && dt != kBF16 && dt != kF16 && dt != kF64)
+    return fail(RAVEL_EM_EINVAL, "payload dtype must be float32/bfloat16/float16/float64 (code %d)", dt);
+  return RAVEL_EM_OK;
+}
+
+int check_ws(const Bump& plan, size_t have) {
+  if (have < plan.off)
+    return fail(RAVEL_EM_EWORKSPACE, "workspace of %zu bytes, need %zu", have, plan.off);
+  return RAVEL_EM_OK;
+}
+
+// Workspace of one sort.
+template <typename U>
+struct SortWs {
+  U* ka;
+  U* kb;
+  uint32_t* counts;
+};
+
+template <typename U>
+SortWs<U> take_sort(Bump& bp, const Tape& tp) {
+  SortWs<U> w;
+  w.ka = bp.take<U>((size_t)tp.n());
+  w.kb = bp.take<U>((size_t)tp.n());
+  w.counts = bp.take<uint32_t>(sort_counts_words(tp));
+  return w;
+}
+
+size_t sort_bytes(const Tape& tp) {
+  Bump bp(nullptr);
+  if (tp.wide())
+    take_sort<uint64_t>(bp, tp);
+  else
+    take_sort<uint32_t>(bp, tp);
+  return bp.off;
+}
+
+// ---------------------------------------------------------- latest-k --
+
+struct LkPlan {
+  int32_t* src;
+};
+
+template <typename U>
+int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+                 const void* payload, int64_t row_bytes, const Tape& tp, int64_t k,
+                 void* out_values, uint8_t* out_mask, int32_t* out_src, void* ws, size_t wsb,
+                 hipStream_t s) {
+  Bump bp(ws);
+  SortWs<U> sw = take_sort<U>(bp, tp);
+  int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
+  if (int rc = check_ws(bp, wsb)) return rc;
+  U* sorted = nullptr;
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
+  if (e != hipSuccess) return hip_fail(e, "sort");
+  if (!raddr && !wmask)
+    e = link_same<U>(sorted, tp, (int)k, src, s);
+  else
+    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+  if (e != hipSuccess) return hip_fail(e, "resolve");
+  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+  if (e != hipSuccess) return hip_fail(e, "gather");
+  return RAVEL_EM_OK;
+}
+
+template <typename U>
+int resolve_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+                const Tape& tp, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
+  Bump bp(ws);
+  SortWs<U> sw = take_sort<U>(bp, tp);
+  if (int rc = check_ws(bp, wsb)) return rc;
+  U* sorted = nullptr;
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
+  if (e != hipSuccess) return hip_fail(e, "sort");
+  if (!raddr && !wmask)
+    e = link_same<U>(sorted, tp, (int)k, src, s);
+  else
+    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+  if (e != hipSuccess) return hip_fail(e, "resolve");
+  return RAVEL_EM_OK;
+}
+
+template <typename U>
+size_t latest_k_ws_t(const Tape& tp, int64_t k, bool want_src) {
+  Bump bp(nullptr);
+  take_sort<U>(bp, tp);
+  if (!want_src) bp.take<int32_t>((size_t)(tp.n() * k));
+  return bp.off;
+}
+
+// ---------------------------------------------------------- seg-sum --
+
+template <typename U>
+struct SumWs {
+  SortWs<U> sw;
+  void* tail;
+  uint8_t* flag;
+  void* carry;
+  void* S;
+  int32_t* spos;
+  void* gacc;
+};
+
+template <typename U>
+SumWs<U> take_sum(Bump& bp, const Tape& tp, int64_t D, int dtype, bool direct, bool backward) {
+  SumWs<U> w{};
+  w.sw = take_sort<U>(bp, tp);
+  const size_t nch = seg_sum_chunks(tp);
+  const size_t ab = acc_bytes(dtype);
+  w.tail = bp.take<char>(nch * (size_t)D * ab);
+  w.flag = bp.take<uint8_t>(nch);
+  w.carry = bp.take<char>(nch * (size_t)D * ab);
+  if (!direct) {
+    w.spos = bp.take<int32_t>((size_t)tp.n());
+    if (backward)
+      w.gacc = bp.take<char>((size_t)tp.n() * (size_t)D * (dtype == kF64 ? 8 : 4));
+    else
+      w.S = bp.take<char>((size_t)tp.n() * (size_t)D * dtype_size(dtype));
+  }
+  return w;
+}
+
+template <typename U>
+int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+                const void* payload, int dtype, const Tape& tp, int64_t D, void* out_sum,
+                uint8_t* out_mask, void* ws, size_t wsb, hipStream_t s) {
+  const bool direct = !raddr && !wmask;
+  Bump bp(ws);
+  SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, false);
+  if (int rc = check_ws(bp, wsb)) return rc;
+  U* sorted = nullptr;
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s);
+  if (e != hipSuccess) return hip_fail(e, "sort");
+  if (direct) {
+    e = seg_sum<U>(sorted, payload, dtype, tp, D, true, out_sum, out_mask, w.tail, w.flag,
+                   w.carry, s);
+    if (e != hipSuccess) return hip_fail(e, "segmented sum");
+    return RAVEL_EM_OK;
+  }
+  e = seg_sum<U>(sorted, payload, dtype, tp, D, false, w.S, nullptr, w.tail, w.flag, w.carry, s);
+  if (e != hipSuccess) return hip_fail(e, "segmented sum");
+  e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
+  if (e != hipSuccess) return hip_fail(e, "resolve");
+  e = gather_rows(w.S, tp.n(), w.spos, tp.n(), D * dtype_size(dtype), out_sum, out_mask, s);
+  if (e != hipSuccess) return hip_fail(e, "gather");
+  return RAVEL_EM_OK;
+}
+
+template <typename U>
+int seg_sum_bwd_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+                    const void* grad, int dtype, const Tape& tp, int64_t D, void* grad_payload,
+                    void* ws, size_t wsb, hipStream_t s) {
+  const bool direct = !raddr && !wmask;
+  Bump bp(ws);
+  SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, true);
+  if (int rc = check_ws(bp, wsb)) return rc;
+  U* sorted = nullptr;
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s);
+  if (e != hipSuccess) return hip_fail(e, "sort");
+  if (!direct) {
+    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
+    if (e != hipSuccess) return hip_fail(e, "resolve");
+  }
+  e = seg_sum_bwd<U>(sorted, w.spos, grad, dtype, tp, D, direct, (float*)w.gacc, w.tail, w.flag,
+                     w.carry, grad_payload, s);
+  if (e != hipSuccess) return hip_fail(e, "segmented sum backward");
+  return RAVEL_EM_OK;
+}
+
+template <typename U>
+size_t sum_ws_t(const Tape& tp, int64_t D, int dtype, bool direct, bool backward) {
+  Bump bp(nullptr);
+  take_sum<U>(bp, tp, D, dtype, direct, backward);
+  return bp.off;
+}
+
+}  // namespace
+
+int bit_width_u64(uint64_t x) {
+  int b = 0;
+  while (x) {
+    ++b;
+    x >>= 1;
+  }
+  return b;
+}
+
+Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode) {
+  Tape tp;
+  tp.B = B;
+  tp.T = T;
+  tp.C = C;
+  tp.A = A;
+  tp.masked = masked;
+  tp.mode = mode;
+  tp.tbits = T > 0 ? bit_width_u64((uint64_t)(T - 1)) : 0;
+  tp.abits = masked ? bit_width_u64((uint64_t)A) : bit_width_u64((uint64_t)(A - 1));
+  const __int128 bound = (__int128)B * C * A * (T + 1);
+  tp.trunc32 = (mode == kWrap) && bound <= (__int128)0x7fffffff;
+  return tp;
+}
+
+}  // namespace rem
+
+using namespace rem;
+
+extern "C" {
+
+const char* ravel_em_last_error(void) { return g_err.c_str(); }
+
+int ravel_em_abi_version(void) { return 1; }
+
+int ravel_em_key_bits(int64_t B, int64_t T, int64_t C, int64_t A) {
+  const __int128 bound = (__int128)B * C * A * (T + 1);
+  return bound <= (__int128)0x7fffffff ? 32 : 64;
+}
+
+size_t ravel_em_sort_order_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int has_mask) {
+  if (check_tape(B, T, C, A)) return 0;
+  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  Bump bp(nullptr);
+  bp.off = sort_bytes(tp);
+  if (has_mask) bp.take<int64_t>((size_t)(B * T + 1));
+  return bp.off;
+}
+
+int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* write_mask,
+                        int64_t B, int64_t T, int64_t C, int64_t A, void* out_sorted_keys,
+                        int64_t* out_order, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!write_addr || !out_sorted_keys || !out_order) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool keys64 = ravel_em_key_bits(B, T, C, A) == 64;
+  auto run = [&](auto tag) -> int {
+    using U = decltype(tag);
+    Bump bp(workspace);
+    SortWs<U> sw = take_sort<U>(bp, tp);
+    int64_t* vprefix = write_mask ? bp.take<int64_t>((size_t)(B * T + 1)) : nullptr;
+    if (int rc = check_ws(bp, workspace_bytes)) return rc;
+    U* sorted = nullptr;
+    hipError_t e = sort_tape<U>(write_addr, addr_dtype == kI64, write_mask, tp, sw.ka, sw.kb,
+                                sw.counts, &sorted, s);
+    if (e != hipSuccess) return hip_fail(e, "sort");
+    e = emit_order<U>(sorted, write_mask, vprefix, tp, out_sorted_keys, keys64, out_order, s);
+    if (e != hipSuccess) return hip_fail(e, "emit order");
+    return RAVEL_EM_OK;
+  };
+  return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+}
+
+size_t ravel_em_latest_k_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
+                                   int has_read, int has_mask, int want_src) {
+  (void)has_read;
+  if (check_tape(B, T, C, A) || k < 1) return 0;
+  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  return tp.wide() ? latest_k_ws_t<uint64_t>(tp, k, want_src != 0)
+                   : latest_k_ws_t<uint32_t>(tp, k, want_src != 0);
+}
+
+int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                          const uint8_t* write_mask, const void* payload, int payload_dtype,
+                          int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, int64_t k,
+                          void* out_values, uint8_t* out_mask, int32_t* out_src, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
+  int64_t nk;
+  if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!write_addr || !payload || !out_values || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
+  const int64_t row_bytes = D * dtype_size(payload_dtype);
+  hipStream_t s = (hipStream_t)stream;
+  const bool a64 = addr_dtype == kI64;
+  if (tp.wide())
+    return latest_k_run<uint64_t>(write_addr, read_addr, a64, write_mask, payload, row_bytes, tp,
+                                  k, out_values, out_mask, out_src, workspace, workspace_bytes, s);
+  return latest_k_run<uint32_t>(write_addr, read_addr, a64, write_mask, payload, row_bytes, tp, k,
+                                out_values, out_mask, out_src, workspace, workspace_bytes, s);
+}
+
+size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
+                                           int has_read, int has_mask) {
+  (void)has_read;
+  if (check_tape(B, T, C, A) || k < 1) return 0;
+  return sort_bytes(make_tape(B, T, C, A, has_mask != 0, kWrap));
+}
+
+int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int addr_dtype,
+                              const uint8_t* write_mask, int64_t B, int64_t T, int64_t C,
+                              int64_t A, int64_t k, int32_t* out_src, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  int64_t nk;
+  if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!write_addr || !out_src) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool a64 = addr_dtype == kI64;
+  if (tp.wide())
+    return resolve_run<uint64_t>(write_addr, read_addr, a64, write_mask, tp, k, out_src, workspace,
+                                 workspace_bytes, s);
+  return resolve_run<uint32_t>(write_addr, read_addr, a64, write_mask, tp, k, out_src, workspace,
+                               workspace_bytes, s);
+}
+
+int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, const int32_t* src,
+                         int64_t n_rows, void* out_values, uint8_t* out_mask, void* stream) {
+  g_err.clear();
+  if (n_src < 0 || n_rows < 0 || row_bytes < 1)
+    return fail(RAVEL_EM_EINVAL, "bad gather sizes n_src=%lld n_rows=%lld row_bytes=%lld",
+                (long long)n_src, (long long)n_rows, (long long)row_bytes);
+  if (n_src > kMaxRecords || n_rows > kMaxRecords) return fail(RAVEL_EM_EINVAL, "row counts must be < 2^31");
+  if (n_rows == 0) return RAVEL_EM_OK;
+  if ((n_src > 0 && !rows) || !src || !out_values) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipError_t e = gather_rows(rows, n_src, src, n_rows, row_bytes, out_values, out_mask,
+                             (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "gather");
+  return RAVEL_EM_OK;
+}
+
+size_t ravel_em_latest_k_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k,
+                                       int payload_dtype, int chain) {
+  (void)k;
+  Bump bp(nullptr);
+  const int64_t N = B * T * C;
+  if (chain)
+    bp.take<int32_t>((size_t)N);
+  else if (payload_dtype == kBF16 || payload_dtype == kF16)
+    bp.take<float>((size_t)(N * D));
+  return bp.off;
+}
+
+int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int payload_dtype,
+                          int64_t B, int64_t T, int64_t C, int64_t D, int64_t k, int chain,
+                          void* grad_payload, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, 1)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (k < 1 || D < 1) return fail(RAVEL_EM_EINVAL, "k and D must be positive");
+  const int64_t N = B * T * C;
+  if (N == 0) return RAVEL_EM_OK;
+  if (!src || !grad_values || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
+  Bump bp(workspace);
+  int32_t* next = nullptr;
+  float* acc = nullptr;
+  if (chain)
+    next = bp.take<int32_t>((size_t)N);
+  else if (payload_dtype == kBF16 || payload_dtype == kF16)
+    acc = bp.take<float>((size_t)(N * D));
+  if (int rc = check_ws(bp, workspace_bytes)) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = chain ? latest_k_bwd_chain(src, grad_values, payload_dtype, N, D, (int)k, next,
+                                            grad_payload, s)
+                       : latest_k_bwd_atomic(src, grad_values, payload_dtype, N, D, (int)k, acc,
+                                             grad_payload, s);
+  if (e != hipSuccess) return hip_fail(e, "latest-k backward");
+  return RAVEL_EM_OK;
+}
+
+size_t ravel_em_seg_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                  int has_read, int has_mask, int payload_dtype) {
+  if (check_tape(B, T, C, A) || D < 1) return 0;
+  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  const bool direct = !has_read && !has_mask;
+  return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, direct, false)
+                   : sum_ws_t<uint32_t>(tp, D, payload_dtype, direct, false);
+}
+
+int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                         const uint8_t* write_mask, const void* payload, int payload_dtype,
+                         int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, void* out_sum,
+                         uint8_t* out_mask, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!write_addr || !payload || !out_sum || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool a64 = addr_dtype == kI64;
+  if (tp.wide())
+    return seg_sum_run<uint64_t>(write_addr, read_addr, a64, write_mask, payload, payload_dtype,
+                                 tp, D, out_sum, out_mask, workspace, workspace_bytes, s);
+  return seg_sum_run<uint32_t>(write_addr, read_addr, a64, write_mask, payload, payload_dtype, tp,
+                               D, out_sum, out_mask, workspace, workspace_bytes, s);
+}
+
+size_t ravel_em_seg_sum_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                      int has_read, int has_mask, int payload_dtype) {
+  if (check_tape(B, T, C, A) || D < 1) return 0;
+  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  const bool direct = !has_read && !has_mask;
+  return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, direct, true)
+                   : sum_ws_t<uint32_t>(tp, D, payload_dtype, direct, true);
+}
+
+int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                         const uint8_t* write_mask, const void* grad_sum, int payload_dtype,
+                         int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                         void* grad_payload, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!write_addr || !grad_sum || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool a64 = addr_dtype == kI64;
+  if (tp.wide())
+    return seg_sum_bwd_run<uint64_t>(write_addr, read_addr, a64, write_mask, grad_sum,
+                                     payload_dtype, tp, D, grad_payload, workspace,
+                                     workspace_bytes, s);
+  return seg_sum_bwd_run<uint32_t>(write_addr, read_addr, a64, write_mask, grad_sum, payload_dtype,
+                                   tp, D, grad_payload, workspace, workspace_bytes, s);
+}
+
+static int check_cache(int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,
+                       int64_t k, int64_t D) {
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (B < 0 || C < 0 || A < 1 || k < 1 || D < 1)
+    return fail(RAVEL_EM_EINVAL, "bad cache shape B=%lld C=%lld A=%lld k=%lld D=%lld",
+                (long long)B, (long long)C, (long long)A, (long long)k, (long long)D);
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_cache_read(const void* values, const uint8_t* filled, const void* addr,
+                        int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,
+                        int64_t k, int64_t D, void* out_values, uint8_t* out_mask, void* stream) {
+  g_err.clear();
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (B * C == 0) return RAVEL_EM_OK;
+  if (!values || !filled || !addr || !out_values || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipError_t e = cache_read(values, filled, addr, addr_dtype == kI64, B * C, A, k,
+                            D * dtype_size(payload_dtype), out_values, out_mask,
+                            (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cache read");
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_cache_write(void* values, uint8_t* filled, const void* addr, int addr_dtype,
+                         const void* payload, int payload_dtype, int64_t B, int64_t C, int64_t A,
+                         int64_t k, int64_t D, void* stream) {
+  g_err.clear();
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (B * C == 0) return RAVEL_EM_OK;
+  if (!values || !filled || !addr || !payload) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipError_t e = cache_write(values, filled, addr, addr_dtype == kI64, payload, B * C, A, k,
+                             D * dtype_size(payload_dtype), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cache write");
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_cache_step(void* values, uint8_t* filled, const void* read_addr,
+                        const void* write_addr, int addr_dtype, const void* payload,
+                        int payload_dtype, int64_t B, int64_t C, int64_t A, int64_t k, int64_t D,
+                        void* out_values, uint8_t* out_mask, void* stream) {
+  g_err.clear();
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (B * C == 0) return RAVEL_EM_OK;
+  if (!values || !filled || !read_addr || !write_addr || !payload || !out_values || !out_mask)
+    return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipError_t e = cache_step(values, filled, read_addr, write_addr, addr_dtype == kI64, payload,
+                            B * C, A, k, D * dtype_size(payload_dtype), out_values, out_mask,
+                            (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cache step");
+  return RAVEL_EM_OK;
+}
+
+size_t ravel_em_cache_prefill_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
+                                        int has_mask) {
+  if (check_tape(B, T, C, A)) return 0;
+  return sort_bytes(make_tape(B, T, C, A, has_mask != 0, kClamp));
+}
+
+int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t* write_mask,
+                           const void* payload, int payload_dtype, int64_t B, int64_t T,
+                           int64_t C, int64_t D, int64_t A, int64_t k, void* values,
+                           uint8_t* filled, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (B * C == 0) return RAVEL_EM_OK;
+  if (!values || !filled || (B * T * C > 0 && (!write_addr || !payload)))
+    return fail(RAVEL_EM_EINVAL, "null pointer");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t row_bytes = D * dtype_size(payload_dtype);
+  auto run = [&](auto tag) -> int {
+    using U = decltype(tag);
+    Bump bp(workspace);
+    SortWs<U> sw = take_sort<U>(bp, tp);
+    if (int rc = check_ws(bp, workspace_bytes)) return rc;
+    U* sorted = nullptr;
+    hipError_t e = hipSuccess;
+    if (tp.n() > 0) {
+      e = sort_tape<U>(write_addr, addr_dtype == kI64, write_mask, tp, sw.ka, sw.kb, sw.counts,
+                       &sorted, s);
+      if (e != hipSuccess) return hip_fail(e, "sort");
+    }
+    e = cache_prefill<U>(sorted, payload, tp, k, row_bytes, values, filled, s);
+    if (e != hipSuccess) return hip_fail(e, "cache prefill");
+    return RAVEL_EM_OK;
+  };
+  return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+}
+
+}  // extern "C"

@@ -1,0 +1,254 @@
+// Latest-value decode cache (gfx950).
+//
+// Replaces RavelLayerCache.read / .write (ravel_lm/ravel_memory.py:271-292) and
+// extends it to k slots: values [B*C, A, k, D], filled [B*C, A, k].  Slot j holds
+// the (j+1)-th most recent write to that address, which is what
+// causal_last_k_lookup returns for a read after the same writes
+// (ravel_memory.py:159-176).  Addresses are clamped to [0, A-1] as in the
+// reference cache (ravel_memory.py:276, :289).
+//
+//  cache_read    gather k slot rows per (b,c), zeroing unfilled slots
+//  cache_write   shift-insert: slot j <- slot j-1, slot 0 <- payload
+//  cache_step    read then write in one launch (reads see the state before the
+//                write, as RavelMemoryLayer.step orders them, model.py:421-424)
+//  cache_prefill build the cache of a whole tape from its sorted runs: the last
+//                k records of every (b,c,a) stream go to slots 0..k-1.
+
+#include "em_common.h"
+
+namespace rem {
+
+namespace {
+
+template <typename AT>
+__device__ __forceinline__ int64_t clamp_addr(const AT* addr, int64_t i, int64_t A) {
+  const int64_t a = (int64_t)addr[i];
+  return a < 0 ? 0 : (a >= A ? A - 1 : a);
+}
+
+template <typename V, typename AT>
+__global__ __launch_bounds__(256) void cache_read_kernel(const V* __restrict__ values,
+                                                        const uint8_t* __restrict__ filled,
+                                                        const AT* __restrict__ addr, int64_t BC,
+                                                        int64_t A, int64_t k, int64_t upr,
+                                                        V* __restrict__ out,
+                                                        uint8_t* __restrict__ omask) {
+  const int64_t total = BC * k * upr;
+  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = g / upr;  // bc*k + j
+    const int64_t v = g - row * upr;
+    const int64_t bc = row / k;
+    const int64_t j = row - bc * k;
+    const int64_t a = clamp_addr(addr, bc, A);
+    const int64_t slot = (bc * A + a) * k + j;
+    const bool f = filled[slot] != 0;
+    V val;
+    if (f) {
+      val = values[slot * upr + v];
+    } else {
+      val = V{};
+    }
+    out[g] = val;
+    if (v == 0) omask[row] = f ? 1 : 0;
+  }
+}
+
+// Block layout shared by write and step: `gpb` (b,c) rows per block, `tpr`
+// threads per row, each thread owns row units v = lid, lid+tpr, ...
+struct RowLayout {
+  int tpr, gpb;
+};
+
+inline RowLayout row_layout(int64_t upr) {
+  int tpr = 1;
+  while (tpr < upr && tpr < 256) tpr <<= 1;
+  return RowLayout{tpr, 256 / tpr};
+}
+
+template <typename V, typename AT, bool READ>
+__global__ __launch_bounds__(256) void cache_rw_kernel(
+    V* __restrict__ values, uint8_t* __restrict__ filled, const AT* __restrict__ raddr,
+    const AT* __restrict__ waddr, const V* __restrict__ payload, int64_t BC, int64_t A, int64_t k,
+    int64_t upr, int tpr, int gpb, V* __restrict__ out, uint8_t* __restrict__ omask) {
+  const int lid = threadIdx.x % tpr;
+  const int64_t bc = (int64_t)blockIdx.x * gpb + threadIdx.x / tpr;
+  const bool active = bc < BC;
+  if (READ) {
+    if (active) {
+      const int64_t ar = clamp_addr(raddr, bc, A);
+      for (int64_t j = 0; j < k; ++j) {
+        const int64_t slot = (bc * A + ar) * k + j;
+        const bool f = filled[slot] != 0;
+        for (int64_t v = lid; v < upr; v += tpr) {
+          V val;
+          if (f) {
+            val = values[slot * upr + v];
+          } else {
+            val = V{};
+          }
+          out[(bc * k + j) * upr + v] = val;
+        }
+        if (lid == 0) omask[bc * k + j] = f ? 1 : 0;
+      }
+    }
+    __syncthreads();  // every read of `filled` precedes the shift below
+  }
+  if (!active) return;
+  const int64_t aw = clamp_addr(waddr, bc, A);
+  const int64_t base = (bc * A + aw) * k;
+  for (int64_t v = lid; v < upr; v += tpr) {
+    for (int64_t j = k - 1; j > 0; --j) values[(base + j) * upr + v] = values[(base + j - 1) * upr + v];
+    values[base * upr + v] = payload[bc * upr + v];
+  }
+  if (lid == 0) {
+    for (int64_t j = k - 1; j > 0; --j) filled[base + j] = filled[base + j - 1];
+    filled[base] = 1;
+  }
+}
+
+template <typename U, typename V>
+__global__ __launch_bounds__(256) void prefill_tail_kernel(const U* __restrict__ sorted,
+                                                          const V* __restrict__ payload,
+                                                          int64_t N, int64_t T, int64_t C,
+                                                          int64_t A, int tbits, int64_t k,
+                                                          int64_t upr, V* __restrict__ values,
+                                                          uint8_t* __restrict__ filled) {
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  const int64_t total = N * upr;
+  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t p = g / upr;
+    const int64_t v = g - p * upr;
+    const int64_t seg = p / T;
+    const int64_t i = p - seg * T;
+    const U u = sorted[p];
+    const U a = u >> tbits;
+    if ((int64_t)a >= A) continue;  // masked write
+    int64_t e = 0;  // later records of the same stream, capped at k
+    while (e < k && i + 1 + e < T && (sorted[p + 1 + e] >> tbits) == a) ++e;
+    if (e >= k) continue;
+    const int64_t b = seg / C;
+    const int64_t c = seg - b * C;
+    const int64_t tt = (int64_t)(u & tmask);
+    if (tt >= T) continue;
+    const int64_t rec = (b * T + tt) * C + c;
+    const int64_t slot = (seg * A + (int64_t)a) * k + e;
+    values[slot * upr + v] = payload[rec * upr + v];
+    if (v == 0) filled[slot] = 1;
+  }
+}
+
+template <typename V>
+hipError_t cache_read_t(const void* values, const uint8_t* filled, const void* addr, bool addr64,
+                        int64_t BC, int64_t A, int64_t k, int64_t upr, void* out, uint8_t* omask,
+                        hipStream_t s) {
+  const unsigned grid = grid_for(BC * k * upr, 256);
+  if (addr64)
+    cache_read_kernel<V, int64_t><<<grid, 256, 0, s>>>((const V*)values, filled,
+                                                       (const int64_t*)addr, BC, A, k, upr,
+                                                       (V*)out, omask);
+  else
+    cache_read_kernel<V, int32_t><<<grid, 256, 0, s>>>((const V*)values, filled,
+                                                       (const int32_t*)addr, BC, A, k, upr,
+                                                       (V*)out, omask);
+  return hipGetLastError();
+}
+
+template <typename V, bool READ>
+hipError_t cache_rw_t(void* values, uint8_t* filled, const void* raddr, const void* waddr,
+                      bool addr64, const void* payload, int64_t BC, int64_t A, int64_t k,
+                      int64_t upr, void* out, uint8_t* omask, hipStream_t s) {
+  const RowLayout L = row_layout(upr);
+  const unsigned grid = (unsigned)((BC + L.gpb - 1) / L.gpb);
+  if (addr64)
+    cache_rw_kernel<V, int64_t, READ><<<grid, 256, 0, s>>>(
+        (V*)values, filled, (const int64_t*)raddr, (const int64_t*)waddr, (const V*)payload, BC,
+        A, k, upr, L.tpr, L.gpb, (V*)out, omask);
+  else
+    cache_rw_kernel<V, int32_t, READ><<<grid, 256, 0, s>>>(
+        (V*)values, filled, (const int32_t*)raddr, (const int32_t*)waddr, (const V*)payload, BC,
+        A, k, upr, L.tpr, L.gpb, (V*)out, omask);
+  return hipGetLastError();
+}
+
+int vec_bytes(uintptr_t align) {
+  if ((align & 15) == 0) return 16;
+  if ((align & 7) == 0) return 8;
+  if ((align & 3) == 0) return 4;
+  if ((align & 1) == 0) return 2;
+  return 1;
+}
+
+}  // namespace
+
+#define REM_VEC_DISPATCH(vb, CALL)                 \
+  switch (vb) {                                    \
+    case 16: { using V = u32x4; return CALL; }     \
+    case 8: { using V = u32x2; return CALL; }      \
+    case 4: { using V = uint32_t; return CALL; }   \
+    case 2: { using V = uint16_t; return CALL; }   \
+    default: { using V = uint8_t; return CALL; }   \
+  }
+
+hipError_t cache_read(const void* values, const uint8_t* filled, const void* addr, bool addr64,
+                      int64_t BC, int64_t A, int64_t k, int64_t row_bytes, void* out,
+                      uint8_t* omask, hipStream_t s) {
+  if (BC == 0) return hipSuccess;
+  const int vb = vec_bytes((uintptr_t)values | (uintptr_t)out | (uintptr_t)row_bytes);
+  REM_VEC_DISPATCH(vb, (cache_read_t<V>(values, filled, addr, addr64, BC, A, k, row_bytes / vb,
+                                        out, omask, s)))
+}
+
+hipError_t cache_write(void* values, uint8_t* filled, const void* addr, bool addr64,
+                       const void* payload, int64_t BC, int64_t A, int64_t k, int64_t row_bytes,
+                       hipStream_t s) {
+  if (BC == 0) return hipSuccess;
+  const int vb = vec_bytes((uintptr_t)values | (uintptr_t)payload | (uintptr_t)row_bytes);
+  REM_VEC_DISPATCH(vb, (cache_rw_t<V, false>(values, filled, nullptr, addr, addr64, payload, BC,
+                                             A, k, row_bytes / vb, nullptr, nullptr, s)))
+}
+
+hipError_t cache_step(void* values, uint8_t* filled, const void* raddr, const void* waddr,
+                      bool addr64, const void* payload, int64_t BC, int64_t A, int64_t k,
+                      int64_t row_bytes, void* out, uint8_t* omask, hipStream_t s) {
+  if (BC == 0) return hipSuccess;
+  const int vb =
+      vec_bytes((uintptr_t)values | (uintptr_t)payload | (uintptr_t)out | (uintptr_t)row_bytes);
+  REM_VEC_DISPATCH(vb, (cache_rw_t<V, true>(values, filled, raddr, waddr, addr64, payload, BC, A,
+                                            k, row_bytes / vb, out, omask, s)))
+}
+
+template <typename U>
+hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, int64_t k,
+                         int64_t row_bytes, void* values, uint8_t* filled, hipStream_t s) {
+  const int64_t BC = tp.nseg();
+  hipError_t e = fill_bytes(values, 0, (size_t)(BC * tp.A * k * row_bytes), s);
+  if (e != hipSuccess) return e;
+  e = fill_bytes(filled, 0, (size_t)(BC * tp.A * k), s);
+  if (e != hipSuccess) return e;
+  const int64_t N = tp.n();
+  if (N == 0) return hipSuccess;
+  const int vb = vec_bytes((uintptr_t)values | (uintptr_t)payload | (uintptr_t)row_bytes);
+  const int64_t upr = row_bytes / vb;
+  const unsigned grid = grid_for(N * upr, 256);
+#define REM_PREFILL(VT)                                                                          \
+  prefill_tail_kernel<U, VT><<<grid, 256, 0, s>>>(sorted, (const VT*)payload, N, tp.T, tp.C,     \
+                                                  tp.A, tp.tbits, k, upr, (VT*)values, filled)
+  switch (vb) {
+    case 16: REM_PREFILL(u32x4); break;
+    case 8: REM_PREFILL(u32x2); break;
+    case 4: REM_PREFILL(uint32_t); break;
+    case 2: REM_PREFILL(uint16_t); break;
+    default: REM_PREFILL(uint8_t); break;
+  }
+#undef REM_PREFILL
+  return hipGetLastError();
+}
+
+template hipError_t cache_prefill<uint32_t>(const uint32_t*, const void*, const Tape&, int64_t,
+                                            int64_t, void*, uint8_t*, hipStream_t);
+template hipError_t cache_prefill<uint64_t>(const uint64_t*, const void*, const Tape&, int64_t,
+                                            int64_t, void*, uint8_t*, hipStream_t);
+
+}  // namespace rem

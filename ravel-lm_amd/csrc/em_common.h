@@ -1,0 +1,181 @@
+// Shared device helpers and internal launcher declarations for the RAVEL
+// event-memory library (gfx950 / CDNA4, wave64).
+//
+// Event tape model (reference: ravel_lm/ravel_memory.py:26-49, :126-176):
+//   every (b, t, c) writes one record into stream (b, c, a) at time t.
+//   A "segment" is the T records of one (b, c) pair.  Inside a segment the
+//   records are sorted by a packed key  u = (a << tbits) | t , which orders
+//   them by (address, time).  Because t is unique inside a segment the packed
+//   key is unique, so the sorted order is unique and equals the order that
+//   torch.sort gives the reference's composite key ((b*C+c)*A+a)*(T+1)+t.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace rem {
+
+constexpr int kWave = 64;
+
+// Native vector types for 16- and 8-byte row units (usable with the
+// non-temporal store builtin, unlike HIP's struct vector types).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Address reduction modes: the lookups wrap with Python remainder
+// (ravel_memory.py:127-128), the decode cache clamps (ravel_memory.py:276,289).
+enum AddrMode : int { kWrap = 0, kClamp = 1 };
+
+// Host-side description of one event tape.
+struct Tape {
+  int64_t B = 0, T = 0, C = 0, A = 0;
+  int tbits = 0;        // bits of the time field in a packed key
+  int abits = 0;        // bits of the address field (includes the mask sentinel A)
+  bool masked = false;  // a write_mask is present: masked records get address A
+  bool trunc32 = false; // reference key dtype is int32: addresses pass through int32 first
+  int mode = kWrap;
+  int64_t nseg() const { return B * C; }
+  int64_t n() const { return B * T * C; }
+  bool wide() const { return abits + tbits > 32; }
+};
+
+int bit_width_u64(uint64_t x);
+Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);
+
+// ---------------------------------------------------------------- device --
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  return (1ull << __lane_id()) - 1ull;
+}
+
+// Lanes of the wave whose 8-bit digit equals this lane's digit.
+__device__ __forceinline__ uint64_t match_byte(uint32_t d) {
+  uint64_t peers = ~0ull;
+#pragma unroll
+  for (int bit = 0; bit < 8; ++bit) {
+    const bool on = (d >> bit) & 1u;
+    const uint64_t m = __ballot(on);
+    peers &= on ? m : ~m;
+  }
+  return peers;
+}
+
+__device__ __forceinline__ int64_t reduce_addr(int64_t a, int64_t A, int mode, bool trunc32) {
+  if (mode == kClamp) return a < 0 ? 0 : (a >= A ? A - 1 : a);
+  if (trunc32) a = (int64_t)(int32_t)(uint32_t)(uint64_t)a;
+  if ((uint64_t)a < (uint64_t)A) return a;
+  const int64_t r = a % A;
+  return r < 0 ? r + A : r;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const unsigned lane = __lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t n = __shfl_up(v, o, kWave);
+    if (lane >= (unsigned)o) v += n;
+  }
+  return v;
+}
+
+// Exclusive scan over the NT threads of a block.  lds must hold NT/64+1 words.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, uint32_t* total) {
+  constexpr int NW = NT / kWave;
+  const int w = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const uint32_t inc = wave_incl_scan(v);
+  if (lane == kWave - 1) lds[w] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t s = 0;
+    for (int i = 0; i < NW; ++i) {
+      const uint32_t x = lds[i];
+      lds[i] = s;
+      s += x;
+    }
+    lds[NW] = s;
+  }
+  __syncthreads();
+  const uint32_t res = inc - v + lds[w];
+  if (total) *total = lds[NW];
+  __syncthreads();
+  return res;
+}
+
+// ------------------------------------------------------------ launchers --
+// All launchers enqueue on `s` and return hipGetLastError() of the last launch.
+
+// Sort every segment of the tape by packed key.  Returns the buffer (ka or kb)
+// holding the sorted keys in *sorted.
+template <typename U>
+hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp,
+                     U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s);
+size_t sort_counts_words(const Tape& tp);
+
+// Emit torch.sort-compatible (sorted_keys, order) for the valid records.
+template <typename U>
+hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, const Tape& tp,
+                      void* out_keys, bool keys64, int64_t* out_order, hipStream_t s);
+
+// Latest-k source indices.  src rows are [N, k] int32, -1 for a missing slot.
+template <typename U>
+hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s);
+template <typename U>
+hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const Tape& tp, int k,
+                        int32_t* src, int32_t* spos, hipStream_t s);
+
+// out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
+hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
+                       int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s);
+
+// Segmented causal sum over sorted runs.
+template <typename U>
+hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& tp, int64_t D,
+                   bool direct, void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag,
+                   void* carry, hipStream_t s);
+size_t seg_sum_chunks(const Tape& tp);
+size_t acc_bytes(int dtype);
+
+// Backward of latest-k: grad_payload[src[r,j]] += grad_values[r,j].
+hipError_t latest_k_bwd_chain(const int32_t* src, const void* grad_values, int dtype, int64_t N,
+                              int64_t D, int k, int32_t* next, void* grad_payload, hipStream_t s);
+hipError_t latest_k_bwd_atomic(const int32_t* src, const void* grad_values, int dtype, int64_t N,
+                               int64_t D, int k, float* acc, void* grad_payload, hipStream_t s);
+
+template <typename U>
+hipError_t seg_sum_bwd(const U* sorted, const int32_t* spos, const void* grad_out, int dtype,
+                       const Tape& tp, int64_t D, bool direct, float* gacc, void* tail,
+                       uint8_t* flag, void* carry, void* grad_payload, hipStream_t s);
+
+// Decode cache (values [B*C, A, k, row], filled [B*C, A, k]).
+hipError_t cache_read(const void* values, const uint8_t* filled, const void* addr, bool addr64,
+                      int64_t BC, int64_t A, int64_t k, int64_t row_bytes, void* out,
+                      uint8_t* omask, hipStream_t s);
+hipError_t cache_write(void* values, uint8_t* filled, const void* addr, bool addr64,
+                       const void* payload, int64_t BC, int64_t A, int64_t k, int64_t row_bytes,
+                       hipStream_t s);
+hipError_t cache_step(void* values, uint8_t* filled, const void* raddr, const void* waddr,
+                      bool addr64, const void* payload, int64_t BC, int64_t A, int64_t k,
+                      int64_t row_bytes, void* out, uint8_t* omask, hipStream_t s);
+template <typename U>
+hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, int64_t k,
+                         int64_t row_bytes, void* values, uint8_t* filled, hipStream_t s);
+hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s);
+
+// dtype codes shared with the C ABI header.
+enum Dtype : int {
+  kI32 = 1, kI64 = 2,
+  kF32 = 10, kBF16 = 11, kF16 = 12, kF64 = 13,
+};
+int dtype_size(int dtype);
+
+inline unsigned grid_for(int64_t work, int block, int64_t cap = 1 << 20) {
+  int64_t g = (work + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+}  // namespace rem

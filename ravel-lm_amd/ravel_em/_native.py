@@ -1,0 +1,135 @@
+"""ctypes binding of the C ABI in include/ravel_em.h.
+
+The shared library ``libravel_em.so`` sits next to this file (built by
+``ravel_em._build``).  There is no fallback: if the library is missing or a
+tensor is not on a ROCm device, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libravel_em.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+# dtype codes (include/ravel_em.h)
+INT32, INT64 = 1, 2
+FLOAT32, BFLOAT16, FLOAT16, FLOAT64 = 10, 11, 12, 13
+
+_PAYLOAD_CODES = {
+    torch.float32: FLOAT32,
+    torch.bfloat16: BFLOAT16,
+    torch.float16: FLOAT16,
+    torch.float64: FLOAT64,
+}
+_ADDR_CODES = {torch.int32: INT32, torch.int64: INT64}
+
+_vp, _i, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+
+# name -> (restype, argtypes); must list every function of include/ravel_em.h
+SIGNATURES = {
+    "ravel_em_last_error": (ctypes.c_char_p, []),
+    "ravel_em_abi_version": (_i, []),
+    "ravel_em_key_bits": (_i, [_i64, _i64, _i64, _i64]),
+    "ravel_em_sort_order_workspace": (_sz, [_i64, _i64, _i64, _i64, _i]),
+    "ravel_em_sort_order": (_i, [_vp, _i, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ravel_em_latest_k_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
+    "ravel_em_latest_k_fwd": (
+        _i,
+        [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "ravel_em_latest_k_resolve_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i]),
+    "ravel_em_latest_k_resolve": (
+        _i, [_vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]
+    ),
+    "ravel_em_gather_rows": (_i, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "ravel_em_latest_k_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i]),
+    "ravel_em_latest_k_bwd": (
+        _i, [_vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i, _vp, _vp, _sz, _vp]
+    ),
+    "ravel_em_seg_sum_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
+    "ravel_em_seg_sum_fwd": (
+        _i, [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]
+    ),
+    "ravel_em_seg_sum_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
+    "ravel_em_seg_sum_bwd": (
+        _i, [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]
+    ),
+    "ravel_em_cache_read": (_i, [_vp, _vp, _vp, _i, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "ravel_em_cache_write": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "ravel_em_cache_step": (
+        _i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]
+    ),
+    "ravel_em_cache_prefill_workspace": (_sz, [_i64, _i64, _i64, _i64, _i]),
+    "ravel_em_cache_prefill": (
+        _i, [_vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]
+    ),
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing or a call into it failed."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def library() -> ctypes.CDLL:
+    """Load libravel_em.so (once) and declare its signatures."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryError(
+                f"{LIB_PATH} is not built; run `python -m ravel_em._build` "
+                "(or __graft_entry__.build()) first"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = library().ravel_em_last_error().decode(errors="replace")
+        raise NativeLibraryError(f"ravel_em error {rc}: {msg}")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def payload_code(dtype: torch.dtype) -> int:
+    code = _PAYLOAD_CODES.get(dtype)
+    if code is None:
+        raise TypeError(f"payload dtype {dtype} is not supported (float32/bfloat16/float16/float64)")
+    return code
+
+
+def addr_code(dtype: torch.dtype) -> int:
+    return _ADDR_CODES[dtype]
+
+
+def require_device(*tensors: Optional[torch.Tensor]) -> None:
+    """The product path runs on ROCm devices only; there is no CPU fallback."""
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "ravel_em runs on ROCm GPU tensors only (got a tensor on "
+                f"{t.device}); there is no CPU fallback"
+            )
+    library()
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,104 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+that include/ravel_em.h declares, and rejects bad arguments before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from ravel_em import _native as nat
+from ravel_em.ravel_memory import _composite_key_dtype
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ravel_em.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ravel_em_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    names = header_functions()
+    assert "ravel_em_latest_k_fwd" in names and "ravel_em_seg_sum_fwd" in names
+    assert len(names) >= 18
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.library()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_binding_table_matches_header():
+    assert sorted(nat.SIGNATURES) == header_functions()
+
+
+def test_abi_version():
+    assert nat.library().ravel_em_abi_version() == 1
+
+
+@pytest.mark.parametrize("shape", [(1, 2048, 3, 1024), (1024, 65536, 64, 65536), (8, 256, 4, 512),
+                                   (4, 65536, 16, 65536), (32, 1024, 8, 1024), (1, 1, 1, 1)])
+def test_key_bits_matches_python_rule(shape):
+    bits = nat.library().ravel_em_key_bits(*shape)
+    assert bits == (32 if _composite_key_dtype(*shape) == torch.int32 else 64)
+
+
+def test_workspace_queries_are_positive_and_monotone():
+    lib = nat.library()
+    small = lib.ravel_em_latest_k_workspace(2, 64, 3, 11, 1, 0, 0, 0)
+    big = lib.ravel_em_latest_k_workspace(4, 65536, 16, 65536, 1, 0, 0, 0)
+    assert 0 < small < big
+    # cfg4: two u32 key buffers + histograms + src
+    N = 4 * 65536 * 16
+    assert big >= 2 * 4 * N + 4 * N
+    assert lib.ravel_em_seg_sum_workspace(4, 65536, 16, 64, 65536, 0, 0, nat.BFLOAT16) > 0
+    assert lib.ravel_em_cache_prefill_workspace(256, 2048, 8, 4096, 0) > 0
+    assert lib.ravel_em_sort_order_workspace(2, 64, 3, 11, 1) > lib.ravel_em_sort_order_workspace(2, 64, 3, 11, 0)
+
+
+def _err():
+    return nat.library().ravel_em_last_error().decode()
+
+
+def test_invalid_arguments_rejected_without_launch():
+    lib = nat.library()
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   2, 3, 4, 5, 0, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "address_space" in _err()
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   2, 3, 4, 5, 7, 0, None, None, None, None, 0, None)
+    assert rc == 1 and "k must be positive" in _err()
+    rc = lib.ravel_em_latest_k_fwd(None, None, 7, None, None, nat.FLOAT32,
+                                   2, 3, 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "address dtype" in _err()
+    rc = lib.ravel_em_seg_sum_fwd(None, None, nat.INT64, None, None, 99,
+                                  2, 3, 4, 5, 7, None, None, None, 0, None)
+    assert rc == 1 and "payload dtype" in _err()
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   1 << 20, 1 << 12, 1 << 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "2^31" in _err()
+    # null pointers with a non-empty tape
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   2, 3, 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "null" in _err()
+    rc = lib.ravel_em_cache_read(None, None, None, nat.INT64, nat.BFLOAT16, 2, 3, 0, 1, 4, None, None, None)
+    assert rc == 1 and "cache shape" in _err()
+
+
+def test_workspace_too_small_is_reported_before_launch():
+    lib = nat.library()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the size check comes first
+    rc = lib.ravel_em_latest_k_fwd(fake, None, nat.INT64, None, fake, nat.FLOAT32,
+                                   2, 64, 3, 4, 11, 1, fake, fake, None, fake, 16, None)
+    assert rc == 3 and "workspace" in _err()
+
+
+def test_empty_tape_is_a_no_op():
+    lib = nat.library()
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   0, 3, 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 0

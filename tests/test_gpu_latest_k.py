@@ -1,0 +1,201 @@
+"""GPU parity of causal_last_k_lookup and the sort order.
+
+Bar: sorted keys/order and latest-k source indices bit-exact to the oracle;
+values are copies, so bit-exact too (missing slots are +0.0; the reference's
+payload*0 can give -0.0, which compares equal).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ravel_em import causal_last_k_lookup, causal_last_k_sources, sort_order, workloads
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+KATS = json.load(open(os.path.join(HERE, "golden", "reference_kats.json")))
+
+
+def expected_values(payload: torch.Tensor, src: np.ndarray) -> torch.Tensor:
+    """Gather on the device from the oracle's source indices (exact copies)."""
+    B, T, C, D = payload.shape
+    s = torch.from_numpy(src.astype(np.int64)).to(payload.device).view(-1)
+    rows = payload.reshape(-1, D).index_select(0, s.clamp_min(0))
+    rows = torch.where((s >= 0).view(-1, 1), rows, torch.zeros((), dtype=rows.dtype, device=rows.device))
+    return rows.view(B, T, C, src.shape[-1], D)
+
+
+def check_against_oracle(write, payload, read=None, *, A, k, mask=None):
+    vals, vmask, src = causal_last_k_sources(write, payload, read, address_space=A, k=k, write_mask=mask)
+    vals2, vmask2 = causal_last_k_lookup(write, payload, read, address_space=A, k=k, write_mask=mask)
+    torch.cuda.synchronize()
+    osrc = oracle.latest_k_src(write, read, address_space=A, k=k, write_mask=mask)
+    gsrc = src.cpu().numpy()
+    bad = np.argwhere(gsrc != osrc)
+    assert bad.size == 0, f"{len(bad)} source mismatches, first at {bad[:3].tolist()}"
+    assert torch.equal(vmask.cpu(), torch.from_numpy(osrc >= 0))
+    assert torch.equal(vals, expected_values(payload, osrc))
+    assert torch.equal(vals2, vals) and torch.equal(vmask2, vmask)
+
+
+# --------------------------------------------- reference tests on the GPU --
+
+
+def test_causal_latest_exact(device):
+    case = KATS["latest_exact"]
+    addr = torch.tensor(case["write"], device=device)
+    payload = torch.tensor(case["payload"], device=device)
+    vals, mask = causal_last_k_lookup(addr, payload, address_space=case["address_space"], k=case["k"])
+    assert not mask[0, 0, 0, 0]
+    assert vals[0, 2, 0, 0, 0].item() == 0.0
+    assert vals[0, 4, 0, 0, 0].item() == 2.0
+    assert vals[0, 4, 0, 1, 0].item() == 0.0
+    _, _, src = causal_last_k_sources(addr, payload, address_space=8, k=2)
+    assert src.cpu().tolist() == case["full_src"]
+
+
+def test_causal_latest_separate_reads_mask_and_payload_gradient(device):
+    # tests/test_memory.py:26-58 of the reference, on the device
+    write = torch.tensor([[[1], [2], [1], [3], [2], [1]]], device=device)
+    read = torch.tensor([[[1], [1], [2], [1], [2], [3]]], device=device)
+    write_mask = torch.tensor([[True, True, False, True, True, True]], device=device)
+    payload = torch.randn(1, 6, 1, 3, device=device, requires_grad=True)
+    actual, actual_mask = causal_last_k_lookup(write, payload, read, address_space=8, k=2, write_mask=write_mask)
+    expected = torch.zeros_like(actual)
+    expected_mask = torch.zeros_like(actual_mask)
+    history = {}
+    for t in range(write.shape[1]):
+        prior = history.get(int(read[0, t, 0]), [])
+        for j, source_t in enumerate(reversed(prior[-2:])):
+            expected[0, t, 0, j] = payload[0, source_t, 0]
+            expected_mask[0, t, 0, j] = True
+        if write_mask[0, t]:
+            history.setdefault(int(write[0, t, 0]), []).append(t)
+    torch.testing.assert_close(actual, expected)
+    assert torch.equal(actual_mask, expected_mask)
+    weights = torch.randn_like(actual)
+    actual_grad = torch.autograd.grad((actual * weights).sum(), payload, retain_graph=True)[0]
+    expected_grad = torch.autograd.grad((expected * weights).sum(), payload)[0]
+    torch.testing.assert_close(actual_grad, expected_grad)
+
+
+def test_bench_forced_repeat(device):
+    case = KATS["bench_forced_repeat"]
+    torch.manual_seed(case["torch_manual_seed"])
+    B, T, C, D, A = case["B"], case["T"], case["C"], case["D"], case["address_space"]
+    addr = torch.randint(0, max(1, A - 1), (B, T, C))
+    payload = torch.randn(B, T, C, D)
+    for t in case["forced_times"]:
+        addr[:, t, :] = A - 1
+    payload[:, case["forced_times"][0]] = case["forced_value"]
+    vals, mask = causal_last_k_lookup(addr.to(device), payload.to(device), address_space=A, k=1)
+    t1 = case["forced_times"][1]
+    assert torch.equal(vals[:, t1, :, 0, :].cpu(), torch.full((B, C, D), case["forced_value"]))
+    assert bool(mask[:, t1, :, 0].all())
+
+
+# --------------------------------------------------------- random parity --
+
+SMALL = [
+    # B, T, C, A, lo, hi, masked, separate reads, k
+    (2, 17, 3, 11, None, None, False, False, 1),
+    (2, 17, 3, 11, None, None, False, True, 1),
+    (3, 40, 2, 5, None, None, True, False, 3),
+    (2, 33, 4, 7, None, None, True, True, 4),
+    (1, 64, 1, 3, -20, 20, False, True, 5),
+    (2, 25, 2, 1, None, None, False, False, 2),
+    (2, 9, 2, 4, None, None, False, False, 12),
+    (1, 30, 3, 6, 2**31 - 10, 2**31 + 10, False, True, 2),
+    (3, 5000, 2, 300, None, None, False, False, 2),  # several sort tiles per segment
+    (1, 70000, 1, 2, None, None, True, False, 3),  # long runs across many tiles
+    (2, 3000, 3, 1 << 21, None, None, False, True, 2),  # 64-bit packed keys (21+12 bits)
+    (2, 257, 5, 100003, None, None, True, True, 1),  # odd sizes, 3 digit passes
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=[str(i) for i in range(len(SMALL))])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_latest_k_parity(device, case, dtype):
+    B, T, C, A, lo, hi, masked, sep, k = case
+    g = torch.Generator().manual_seed(B * 1000 + T + k)
+    lo = 0 if lo is None else lo
+    hi = A if hi is None else hi
+    w = torch.randint(lo, hi, (B, T, C), generator=g)
+    r = torch.randint(lo, hi, (B, T, C), generator=g) if sep else None
+    m = (torch.rand(B, T, generator=g) < 0.6) if masked else None
+    p = torch.randn(B, T, C, 5, generator=g).to(dtype)
+    check_against_oracle(w.to(device), p.to(device), None if r is None else r.to(device),
+                         A=A, k=k, mask=None if m is None else m.to(device))
+
+
+@pytest.mark.parametrize("addr_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("D,dtype", [(1, torch.float32), (3, torch.float16), (8, torch.bfloat16), (33, torch.float64)])
+def test_latest_k_dtypes_and_row_widths(device, addr_dtype, D, dtype):
+    g = torch.Generator().manual_seed(D)
+    B, T, C, A = 2, 300, 3, 17
+    w = torch.randint(0, A, (B, T, C), generator=g).to(addr_dtype)
+    r = torch.randint(0, A, (B, T, C), generator=g).to(addr_dtype)
+    p = torch.randn(B, T, C, D, generator=g).to(dtype)
+    check_against_oracle(w.to(device), p.to(device), r.to(device), A=A, k=3)
+    check_against_oracle(w.to(device), p.to(device), None, A=A, k=2)
+
+
+def test_sort_order_bit_exact(device):
+    for (B, T, C, A, masked) in [(2, 17, 3, 11, False), (3, 40, 2, 5, True), (2, 3000, 3, 1 << 21, False),
+                                 (2, 257, 5, 100003, True), (4, 4096, 8, 4096, False)]:
+        g = torch.Generator().manual_seed(T)
+        w = torch.randint(-A, 2 * A, (B, T, C), generator=g)
+        m = (torch.rand(B, T, generator=g) < 0.5) if masked else None
+        keys, order = sort_order(w.to(device), address_space=A, write_mask=None if m is None else m.to(device))
+        okeys, oorder = oracle.sort_order(w, address_space=A, write_mask=m)
+        assert keys.dtype == (torch.int32 if oracle.key_bits(B, T, C, A) == 32 else torch.int64)
+        assert np.array_equal(keys.cpu().numpy().astype(np.int64), okeys)
+        assert np.array_equal(order.cpu().numpy(), oorder)
+
+
+def test_all_writes_masked_gives_zeros(device):
+    w = torch.randint(0, 5, (2, 8, 3), device=device)
+    p = torch.randn(2, 8, 3, 4, device=device)
+    m = torch.zeros(2, 8, dtype=torch.bool, device=device)
+    vals, mask = causal_last_k_lookup(w, p, address_space=5, k=2, write_mask=m)
+    assert not mask.any() and not vals.any()
+    keys, order = sort_order(w, address_space=5, write_mask=m)
+    assert keys.numel() == 0 and order.numel() == 0
+
+
+def test_empty_tape(device):
+    w = torch.zeros(0, 8, 3, dtype=torch.long, device=device)
+    p = torch.zeros(0, 8, 3, 4, device=device)
+    vals, mask = causal_last_k_lookup(w, p, address_space=5, k=2)
+    assert vals.shape == (0, 8, 3, 2, 4) and mask.shape == (0, 8, 3, 2)
+
+
+# ------------------------------------------------- BASELINE configurations --
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg1b", "cfg2_f32", "cfg2_bf16", "cfg3", "cfg4", "cfg4_adv"])
+def test_baseline_config_parity(device, name):
+    print(f"[parity] {name}", flush=True)
+    if name == "cfg1":
+        w = workloads.cfg1(device)
+    elif name == "cfg1b":
+        w = workloads.cfg1(device, variant="1b")
+    elif name == "cfg2_f32":
+        w = workloads.cfg2(device, torch.float32)
+    elif name == "cfg2_bf16":
+        w = workloads.cfg2(device, torch.bfloat16)
+    elif name == "cfg3":
+        w = workloads.cfg3(device)
+    elif name == "cfg4":
+        w = workloads.cfg4(device)
+    else:
+        w = workloads.cfg4(device, adversarial=True)
+    check_against_oracle(w.write, w.payload, w.read, A=w.address_space, k=w.k)
+    if name in ("cfg2_f32", "cfg4"):
+        keys, order = sort_order(w.write, address_space=w.address_space)
+        okeys, oorder = oracle.sort_order(w.write, address_space=w.address_space)
+        assert np.array_equal(keys.cpu().numpy().astype(np.int64), okeys)
+        assert np.array_equal(order.cpu().numpy(), oorder)
