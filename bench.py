@@ -125,35 +125,54 @@ def main():
         wall = time.perf_counter() - wall0
         ms = t_begin.elapsed_time(t_end) / args.steps
 
-        # Timed region B: the same kernels as resolve + gather calls, with HIP
-        # events around the gather on its launch stream (torch's current stream).
+        # Timed region B: the same call with the library's stage timer on, which
+        # brackets each stage (sort, resolve, gather) with HIP events on the
+        # stream the kernels are launched on.
+        import ctypes
+
         lib = nat.library()
-        stream = torch.cuda.current_stream(dev)
-        src = torch.empty(B, T, C, k, dtype=torch.int32, device=dev)
-        vals_b = torch.empty_like(vals)
-        mask_b = torch.empty_like(mask)
-        ws = nat.workspace(lib.ravel_em_latest_k_resolve_workspace(B, T, C, A, k, 0, 0), dev)
-        row_bytes = D * w.payload.element_size()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)]
+        nat.check(lib.ravel_em_profile_start())
         b_begin = torch.cuda.Event(enable_timing=True)
         b_end = torch.cuda.Event(enable_timing=True)
         b_begin.record()
-        for e0, e1 in ev:
-            nat.check(lib.ravel_em_latest_k_resolve(
-                w.write.data_ptr(), None, nat.INT64, None, B, T, C, A, k, src.data_ptr(),
-                ws.data_ptr(), ws.numel(), stream.cuda_stream))
-            e0.record(stream)
-            nat.check(lib.ravel_em_gather_rows(
-                w.payload.data_ptr(), N, row_bytes, src.data_ptr(), N * k, vals_b.data_ptr(),
-                mask_b.data_ptr(), stream.cuda_stream))
-            e1.record(stream)
+        for _ in range(args.steps):
+            vals_b, mask_b = causal_last_k_lookup(w.write, w.payload, w.read, address_space=A, k=k)
         b_end.record()
+        stage_ms = (ctypes.c_double * 5)()
+        stage_calls = (ctypes.c_int * 5)()
+        nat.check(lib.ravel_em_profile_stop(stage_ms, stage_calls, 5))
         torch.cuda.synchronize()
-        gather_ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / len(ev)
-        split_ms = b_begin.elapsed_time(b_end) / args.steps
-        assert torch.equal(vals_b, vals) and torch.equal(mask_b, mask), "split path differs from fused call"
+        stages = {name: stage_ms[i] / max(1, stage_calls[i])
+                  for i, name in enumerate(["sort", "resolve", "gather"])}
+        gather_ms = stages["gather"]
+        timed_ms = b_begin.elapsed_time(b_end) / args.steps
+        assert torch.equal(vals_b, vals) and torch.equal(mask_b, mask), "repeat call differs"
         valid_slots = int(mask.sum().item())
+        row_bytes = D * w.payload.element_size()
+
+        # Streaming references on the same device: a 512 MiB device-to-device
+        # copy and a 512 MiB fill, the practical HBM ceilings for read+write and
+        # write-only traffic.
+        src_buf = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev).normal_()
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(3):
+            dst_buf.copy_(src_buf)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst_buf.copy_(src_buf)
+        e1.record()
+        torch.cuda.synchronize()
+        copy_gbps = 2 * src_buf.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        dst_buf.fill_(1.0)  # first use loads the kernel: keep it out of the timing
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            dst_buf.fill_(1.0)
+        e1.record()
+        torch.cuda.synchronize()
+        fill_gbps = dst_buf.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        del src_buf, dst_buf
 
     # Gather kernel bytes: src read (4 B/slot), values + mask written, and one
     # payload row read per valid slot.
@@ -206,9 +225,11 @@ def main():
             "unit": "GB/s",
             "frac": op_gbps / PEAK_HBM_GBPS,
             "bytes_per_call": op_bytes,
-            "split_path_ms_per_step": split_ms,
+            "stage_ms": stages,
+            "ms_per_step_with_stage_timer": timed_ms,
         },
         "wall_s_timed_region": wall,
+        "hbm_reference_GBps": {"copy_512MiB": copy_gbps, "fill_512MiB": fill_gbps},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)

@@ -50,6 +50,24 @@ const char* ravel_em_last_error(void);
 int ravel_em_abi_version(void);
 
 /*
+ * Opt-in stage timing of the calls this thread makes.  ravel_em_profile_start()
+ * enables it: every stage (0 sort, 1 resolve, 2 gather, 3 segmented sum,
+ * 4 cache) is then bracketed by HIP events on its stream.
+ * ravel_em_profile_stop() waits for those events, writes the summed
+ * milliseconds and call count of the first n stages, and disables timing.
+ */
+int ravel_em_profile_start(void);
+int ravel_em_profile_stop(double* ms, int* calls, int n);
+
+/*
+ * Sort implementation for the calls this thread makes: 0 (default) picks the
+ * fused pack/look-back sort whenever its LDS budget holds, 1 always uses the
+ * generic multi-kernel sort.  Both produce the same order; the switch exists
+ * so the two can be checked against each other.
+ */
+int ravel_em_set_sort_path(int path);
+
+/*
  * Key width rule of _composite_key_dtype (ravel_lm/ravel_memory.py:45-49):
  * returns 32 when B*C*A*(T+1) <= 2^31-1, else 64.
  */

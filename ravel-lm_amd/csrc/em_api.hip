@@ -5,6 +5,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/ravel_em.h"
 #include "em_common.h"
@@ -14,6 +16,26 @@ namespace rem {
 namespace {
 
 thread_local std::string g_err;
+
+// Stage timing: events come from a per-thread pool that grows on demand and is
+// reused across profile_start/stop pairs.
+struct Profiler {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
+  int open[kStages] = {};
+  std::vector<std::pair<int, std::pair<size_t, size_t>>> spans;
+  size_t take() {
+    if (used == pool.size()) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return (size_t)-1;
+      pool.push_back(e);
+    }
+    return used++;
+  }
+};
+thread_local Profiler g_prof;
+thread_local int g_sort_path = 0;  // 0 automatic, 1 generic multi-kernel sort
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -117,19 +139,29 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
                  const void* payload, int64_t row_bytes, const Tape& tp, int64_t k,
                  void* out_values, uint8_t* out_mask, int32_t* out_src, void* ws, size_t wsb,
                  hipStream_t s) {
+  const bool link = !raddr && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
-  int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
+  int32_t* src = (link || !out_src) ? bp.take<int32_t>((size_t)(tp.n() * k)) : out_src;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
+  stage_begin(kStageSort, s);
   hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
+  stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
-  if (!raddr && !wmask)
+  stage_begin(kStageResolve, s);
+  if (link)
     e = link_same<U>(sorted, tp, (int)k, src, s);
   else
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+  stage_end(kStageResolve, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
-  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+  stage_begin(kStageGather, s);
+  if (link)
+    e = gather_rows_segmajor(payload, src, tp, (int)k, row_bytes, out_values, out_mask, out_src, s);
+  else
+    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+  stage_end(kStageGather, s);
   if (e != hipSuccess) return hip_fail(e, "gather");
   return RAVEL_EM_OK;
 }
@@ -137,25 +169,29 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
 template <typename U>
 int resolve_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
                 const Tape& tp, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
+  const bool link = !raddr && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
+  int32_t* src_seg = link ? bp.take<int32_t>((size_t)(tp.n() * k)) : nullptr;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
-  if (!raddr && !wmask)
-    e = link_same<U>(sorted, tp, (int)k, src, s);
-  else
+  if (link) {
+    e = link_same<U>(sorted, tp, (int)k, src_seg, s);
+    if (e == hipSuccess) e = src_record_major(src_seg, tp, (int)k, src, s);
+  } else {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+  }
   if (e != hipSuccess) return hip_fail(e, "resolve");
   return RAVEL_EM_OK;
 }
 
 template <typename U>
-size_t latest_k_ws_t(const Tape& tp, int64_t k, bool want_src) {
+size_t latest_k_ws_t(const Tape& tp, int64_t k, bool link, bool want_src) {
   Bump bp(nullptr);
   take_sort<U>(bp, tp);
-  if (!want_src) bp.take<int32_t>((size_t)(tp.n() * k));
+  if (link || !want_src) bp.take<int32_t>((size_t)(tp.n() * k));
   return bp.off;
 }
 
@@ -200,11 +236,15 @@ int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, false);
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
+  stage_begin(kStageSort, s);
   hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s);
+  stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (direct) {
+    stage_begin(kStageSum, s);
     e = seg_sum<U>(sorted, payload, dtype, tp, D, true, out_sum, out_mask, w.tail, w.flag,
                    w.carry, s);
+    stage_end(kStageSum, s);
     if (e != hipSuccess) return hip_fail(e, "segmented sum");
     return RAVEL_EM_OK;
   }
@@ -247,6 +287,22 @@ size_t sum_ws_t(const Tape& tp, int64_t D, int dtype, bool direct, bool backward
 
 }  // namespace
 
+void stage_begin(int stage, hipStream_t s) {
+  if (!g_prof.on) return;
+  const size_t i = g_prof.take();
+  if (i == (size_t)-1) return;
+  hipEventRecord(g_prof.pool[i], s);
+  g_prof.open[stage] = (int)i;
+}
+
+void stage_end(int stage, hipStream_t s) {
+  if (!g_prof.on) return;
+  const size_t i = g_prof.take();
+  if (i == (size_t)-1) return;
+  hipEventRecord(g_prof.pool[i], s);
+  g_prof.spans.push_back({stage, {(size_t)g_prof.open[stage], i}});
+}
+
 int bit_width_u64(uint64_t x) {
   int b = 0;
   while (x) {
@@ -268,6 +324,7 @@ Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode
   tp.abits = masked ? bit_width_u64((uint64_t)A) : bit_width_u64((uint64_t)(A - 1));
   const __int128 bound = (__int128)B * C * A * (T + 1);
   tp.trunc32 = (mode == kWrap) && bound <= (__int128)0x7fffffff;
+  tp.fused = g_sort_path == 0;
   return tp;
 }
 
@@ -280,6 +337,44 @@ extern "C" {
 const char* ravel_em_last_error(void) { return g_err.c_str(); }
 
 int ravel_em_abi_version(void) { return 1; }
+
+int ravel_em_set_sort_path(int path) {
+  g_err.clear();
+  if (path != 0 && path != 1) return fail(RAVEL_EM_EINVAL, "sort path must be 0 (automatic) or 1 (generic)");
+  g_sort_path = path;
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_profile_start(void) {
+  g_err.clear();
+  g_prof.on = true;
+  g_prof.used = 0;
+  g_prof.spans.clear();
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_profile_stop(double* ms, int* calls, int n) {
+  g_err.clear();
+  g_prof.on = false;
+  for (int i = 0; i < n; ++i) {
+    if (ms) ms[i] = 0.0;
+    if (calls) calls[i] = 0;
+  }
+  for (const auto& sp : g_prof.spans) {
+    hipEvent_t a = g_prof.pool[sp.second.first], b = g_prof.pool[sp.second.second];
+    hipError_t e = hipEventSynchronize(b);
+    if (e != hipSuccess) return hip_fail(e, "profile");
+    float t = 0.f;
+    e = hipEventElapsedTime(&t, a, b);
+    if (e != hipSuccess) return hip_fail(e, "profile");
+    if (sp.first < n) {
+      if (ms) ms[sp.first] += t;
+      if (calls) calls[sp.first] += 1;
+    }
+  }
+  g_prof.spans.clear();
+  return RAVEL_EM_OK;
+}
 
 int ravel_em_key_bits(int64_t B, int64_t T, int64_t C, int64_t A) {
   const __int128 bound = (__int128)B * C * A * (T + 1);
@@ -326,11 +421,11 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
 
 size_t ravel_em_latest_k_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
                                    int has_read, int has_mask, int want_src) {
-  (void)has_read;
   if (check_tape(B, T, C, A) || k < 1) return 0;
   const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
-  return tp.wide() ? latest_k_ws_t<uint64_t>(tp, k, want_src != 0)
-                   : latest_k_ws_t<uint32_t>(tp, k, want_src != 0);
+  const bool link = !has_read && !has_mask;
+  return tp.wide() ? latest_k_ws_t<uint64_t>(tp, k, link, want_src != 0)
+                   : latest_k_ws_t<uint32_t>(tp, k, link, want_src != 0);
 }
 
 int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
@@ -362,9 +457,12 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
 
 size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
                                            int has_read, int has_mask) {
-  (void)has_read;
   if (check_tape(B, T, C, A) || k < 1) return 0;
-  return sort_bytes(make_tape(B, T, C, A, has_mask != 0, kWrap));
+  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  Bump bp(nullptr);
+  bp.off = sort_bytes(tp);
+  if (!has_read && !has_mask) bp.take<int32_t>((size_t)(tp.n() * k));
+  return bp.off;
 }
 
 int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int addr_dtype,

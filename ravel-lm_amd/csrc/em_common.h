@@ -35,6 +35,7 @@ struct Tape {
   bool masked = false;  // a write_mask is present: masked records get address A
   bool trunc32 = false; // reference key dtype is int32: addresses pass through int32 first
   int mode = kWrap;
+  bool fused = true;    // use the fused sort when its LDS budget holds
   int64_t nseg() const { return B * C; }
   int64_t n() const { return B * T * C; }
   bool wide() const { return abits + tbits > 32; }
@@ -44,6 +45,21 @@ int bit_width_u64(uint64_t x);
 Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);
 
 // ---------------------------------------------------------------- device --
+
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each
+// with a private L2.  With a grid that is a multiple of 8, this maps hardware
+// block ids to logical ids so that each XCD works on one contiguous eighth of
+// the logical blocks (neighbouring data stays in one L2).
+constexpr int kXcds = 8;
+__device__ __forceinline__ uint32_t xcd_block(uint32_t bid, uint32_t nblk) {
+  return (bid % kXcds) * (nblk / kXcds) + bid / kXcds;
+}
+inline unsigned xcd_grid(int64_t work, int block, int64_t cap = 1 << 20) {
+  int64_t g = (work + block - 1) / block;
+  if (g > cap) g = cap;
+  g = (g + kXcds - 1) / kXcds * kXcds;
+  return (unsigned)(g < kXcds ? kXcds : g);
+}
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
   return (1ull << __lane_id()) - 1ull;
@@ -113,15 +129,17 @@ template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp,
                      U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s);
 size_t sort_counts_words(const Tape& tp);
+size_t sort_fused_words(const Tape& tp, size_t key_bytes);
 
 // Emit torch.sort-compatible (sorted_keys, order) for the valid records.
 template <typename U>
 hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, const Tape& tp,
                       void* out_keys, bool keys64, int64_t* out_order, hipStream_t s);
 
-// Latest-k source indices.  src rows are [N, k] int32, -1 for a missing slot.
+// Latest-k source indices, int32, -1 for a missing slot.  link_same writes them
+// segment-major ([B,C,T,k]); search_reads writes record-major ([B,T,C,k]).
 template <typename U>
-hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s);
+hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s);
 template <typename U>
 hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const Tape& tp, int k,
                         int32_t* src, int32_t* spos, hipStream_t s);
@@ -129,6 +147,18 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
 // out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s);
+// Same, with src segment-major ([B,C,T,k]) and out/mask record-major; src_out
+// (optional) receives the sources record-major.
+hipError_t gather_rows_segmajor(const void* rows, const int32_t* src_seg, const Tape& tp, int k,
+                                int64_t row_bytes, void* out, uint8_t* mask, int32_t* src_out,
+                                hipStream_t s);
+hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
+                            hipStream_t s);
+// Opt-in per-stage timing (host side): brackets each stage with HIP events on
+// its stream while enabled.
+enum Stage : int { kStageSort = 0, kStageResolve, kStageGather, kStageSum, kStageCache, kStages };
+void stage_begin(int stage, hipStream_t s);
+void stage_end(int stage, hipStream_t s);
 
 // Segmented causal sum over sorted runs.
 template <typename U>

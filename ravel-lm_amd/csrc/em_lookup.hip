@@ -23,11 +23,15 @@ namespace {
 
 template <typename U>
 __global__ __launch_bounds__(256) void link_same_kernel(const U* __restrict__ sorted, int64_t N,
-                                                       int64_t T, int64_t C, int tbits, int k,
-                                                       int32_t* __restrict__ src) {
+                                                       int64_t T, int k,
+                                                       int32_t* __restrict__ src_seg, int tbits,
+                                                       int64_t C) {
+  // Sorted position p of segment seg writes the k source slots of its record
+  // at src_seg[(seg*T + t)*k + j]: every segment's writes stay inside its own
+  // T*k*4 bytes, and xcd_block keeps a segment's blocks on one XCD.
   const U tmask = (U)((((uint64_t)1) << tbits) - 1);
-  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < N;
-       p += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  for (int64_t p = lb * blockDim.x + threadIdx.x; p < N; p += (int64_t)gridDim.x * blockDim.x) {
     const uint32_t seg = (uint32_t)((uint64_t)p / (uint64_t)T);
     const int64_t i = p - (int64_t)seg * T;
     const uint32_t b = seg / (uint32_t)C;
@@ -36,7 +40,7 @@ __global__ __launch_bounds__(256) void link_same_kernel(const U* __restrict__ so
     const U a = u >> tbits;
     const int64_t t = (int64_t)(u & tmask);
     if (t >= T) continue;
-    int32_t* o = src + (((int64_t)b * T + t) * C + c) * k;
+    int32_t* o = src_seg + ((int64_t)seg * T + t) * k;
     bool alive = true;
     for (int j = 0; j < k; ++j) {
       int32_t v = -1;
@@ -104,52 +108,126 @@ __global__ __launch_bounds__(256) void search_reads_kernel(
   }
 }
 
-template <typename V, int SHIFT>
+// Each block copies a contiguous run of row units; every thread keeps kIlp
+// independent 16-byte loads in flight.  SEG selects a segment-major src.
+constexpr int kIlp = 4;
+
+template <typename V, int SHIFT, bool SEG>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ rows,
                                                          const int32_t* __restrict__ src,
                                                          int64_t nrows, int upr, int64_t nsrc,
+                                                         int64_t T, int64_t C, int k,
                                                          V* __restrict__ out,
-                                                         uint8_t* __restrict__ mask) {
+                                                         uint8_t* __restrict__ mask,
+                                                         int32_t* __restrict__ src_out) {
   const int64_t total = nrows * upr;
-  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < total;
-       g += (int64_t)gridDim.x * blockDim.x) {
-    int64_t row;
-    int v;
-    if (SHIFT >= 0) {
-      row = g >> SHIFT;
-      v = (int)(g & ((1 << SHIFT) - 1));
-    } else {
-      row = g / upr;
-      v = (int)(g - row * upr);
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t step = (int64_t)gridDim.x * blockDim.x * kIlp;
+  for (int64_t base = lb * blockDim.x * kIlp + threadIdx.x; base < total; base += step) {
+    int32_t s[kIlp];
+    int64_t row[kIlp];
+    int v[kIlp];
+#pragma unroll
+    for (int i = 0; i < kIlp; ++i) {
+      const int64_t g = base + (int64_t)i * blockDim.x;
+      if (SHIFT >= 0) {
+        row[i] = g >> SHIFT;
+        v[i] = (int)(g & ((1 << SHIFT) - 1));
+      } else {
+        row[i] = g / upr;
+        v[i] = (int)(g - row[i] * upr);
+      }
+      s[i] = -1;
+      if (g < total) {
+        int64_t srow = row[i];
+        if (SEG) {  // record-major row (b,t,c,j) -> segment-major (b,c,t,j)
+          const int64_t r = row[i] / k;
+          const int64_t j = row[i] - r * k;
+          const int64_t TC = T * C;
+          const int64_t b = r / TC;
+          const int64_t tc = r - b * TC;
+          const int64_t t = tc / C;
+          const int64_t c = tc - t * C;
+          srow = (((b * C + c) * T) + t) * k + j;
+        }
+        s[i] = src[srow];
+      }
     }
-    const int32_t s = src[row];
-    V val;
-    if (s >= 0 && s < nsrc) {
-      val = rows[(int64_t)s * upr + v];
-    } else {
-      val = V{};
+    V val[kIlp];
+#pragma unroll
+    for (int i = 0; i < kIlp; ++i) {
+      if (s[i] >= 0 && s[i] < nsrc) {
+        val[i] = rows[(int64_t)s[i] * upr + v[i]];
+      } else {
+        val[i] = V{};
+      }
     }
-    __builtin_nontemporal_store(val, &out[g]);
-    if (v == 0 && mask) mask[row] = s >= 0 ? 1 : 0;
+#pragma unroll
+    for (int i = 0; i < kIlp; ++i) {
+      const int64_t g = base + (int64_t)i * blockDim.x;
+      if (g < total) {
+        __builtin_nontemporal_store(val[i], &out[g]);
+        if (v[i] == 0) {
+          if (mask) mask[row[i]] = s[i] >= 0 ? 1 : 0;
+          if (SEG && src_out) src_out[row[i]] = s[i];
+        }
+      }
+    }
   }
 }
 
-template <typename V>
+template <typename V, bool SEG>
 hipError_t gather_typed(const void* rows, const int32_t* src, int64_t nrows, int upr, int64_t nsrc,
-                        void* out, uint8_t* mask, hipStream_t s) {
-  const unsigned grid = grid_for(nrows * upr, 256);
+                        int64_t T, int64_t C, int k, void* out, uint8_t* mask, int32_t* src_out,
+                        hipStream_t s) {
+  const unsigned grid = xcd_grid(nrows * upr, 256 * kIlp);
   const V* r = (const V*)rows;
   V* o = (V*)out;
+#define REM_G(SH) gather_rows_kernel<V, SH, SEG><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, T, C, k, o, mask, src_out)
   switch (upr) {
-    case 1: gather_rows_kernel<V, 0><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    case 2: gather_rows_kernel<V, 1><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    case 4: gather_rows_kernel<V, 2><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    case 8: gather_rows_kernel<V, 3><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    case 16: gather_rows_kernel<V, 4><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    case 32: gather_rows_kernel<V, 5><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
-    default: gather_rows_kernel<V, -1><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask); break;
+    case 1: REM_G(0); break;
+    case 2: REM_G(1); break;
+    case 4: REM_G(2); break;
+    case 8: REM_G(3); break;
+    case 16: REM_G(4); break;
+    case 32: REM_G(5); break;
+    default: REM_G(-1); break;
   }
+#undef REM_G
   return hipGetLastError();
+}
+
+template <bool SEG>
+hipError_t gather_dispatch(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
+                           int64_t row_bytes, int64_t T, int64_t C, int k, void* out,
+                           uint8_t* mask, int32_t* src_out, hipStream_t s) {
+  if (nrows == 0) return hipSuccess;
+  const uintptr_t align = (uintptr_t)rows | (uintptr_t)out | (uintptr_t)row_bytes;
+  if ((align & 15) == 0)
+    return gather_typed<u32x4, SEG>(rows, src, nrows, (int)(row_bytes / 16), nsrc, T, C, k, out, mask, src_out, s);
+  if ((align & 7) == 0)
+    return gather_typed<u32x2, SEG>(rows, src, nrows, (int)(row_bytes / 8), nsrc, T, C, k, out, mask, src_out, s);
+  if ((align & 3) == 0)
+    return gather_typed<uint32_t, SEG>(rows, src, nrows, (int)(row_bytes / 4), nsrc, T, C, k, out, mask, src_out, s);
+  if ((align & 1) == 0)
+    return gather_typed<uint16_t, SEG>(rows, src, nrows, (int)(row_bytes / 2), nsrc, T, C, k, out, mask, src_out, s);
+  return gather_typed<uint8_t, SEG>(rows, src, nrows, (int)row_bytes, nsrc, T, C, k, out, mask, src_out, s);
+}
+
+__global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __restrict__ src_seg,
+                                                              int64_t rows, int64_t T, int64_t C,
+                                                              int k, int32_t* __restrict__ out) {
+  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < rows;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = g / k;
+    const int64_t j = g - r * k;
+    const int64_t TC = T * C;
+    const int64_t b = r / TC;
+    const int64_t tc = r - b * TC;
+    const int64_t t = tc / C;
+    const int64_t c = tc - t * C;
+    out[g] = src_seg[(((b * C + c) * T) + t) * k + j];
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n,
@@ -181,9 +259,9 @@ hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s) {
 }
 
 template <typename U>
-hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s) {
+hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s) {
   const int64_t N = tp.n();
-  link_same_kernel<U><<<grid_for(N, 256), 256, 0, s>>>(sorted, N, tp.T, tp.C, tp.tbits, k, src);
+  link_same_kernel<U><<<xcd_grid(N, 256), 256, 0, s>>>(sorted, N, tp.T, k, src_seg, tp.tbits, tp.C);
   return hipGetLastError();
 }
 
@@ -203,15 +281,23 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
   return hipGetLastError();
 }
 
+hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
+                            hipStream_t s) {
+  const int64_t rows = tp.n() * k;
+  src_record_major_kernel<<<grid_for(rows, 256), 256, 0, s>>>(src_seg, rows, tp.T, tp.C, k, out);
+  return hipGetLastError();
+}
+
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s) {
-  if (nrows == 0) return hipSuccess;
-  const uintptr_t align = (uintptr_t)rows | (uintptr_t)out | (uintptr_t)row_bytes;
-  if ((align & 15) == 0) return gather_typed<u32x4>(rows, src, nrows, (int)(row_bytes / 16), nsrc, out, mask, s);
-  if ((align & 7) == 0) return gather_typed<u32x2>(rows, src, nrows, (int)(row_bytes / 8), nsrc, out, mask, s);
-  if ((align & 3) == 0) return gather_typed<uint32_t>(rows, src, nrows, (int)(row_bytes / 4), nsrc, out, mask, s);
-  if ((align & 1) == 0) return gather_typed<uint16_t>(rows, src, nrows, (int)(row_bytes / 2), nsrc, out, mask, s);
-  return gather_typed<uint8_t>(rows, src, nrows, (int)row_bytes, nsrc, out, mask, s);
+  return gather_dispatch<false>(rows, nsrc, src, nrows, row_bytes, 1, 1, 1, out, mask, nullptr, s);
+}
+
+hipError_t gather_rows_segmajor(const void* rows, const int32_t* src_seg, const Tape& tp, int k,
+                                int64_t row_bytes, void* out, uint8_t* mask, int32_t* src_out,
+                                hipStream_t s) {
+  return gather_dispatch<true>(rows, tp.n(), src_seg, tp.n() * k, row_bytes, tp.T, tp.C, k, out,
+                               mask, src_out, s);
 }
 
 template hipError_t link_same<uint32_t>(const uint32_t*, const Tape&, int, int32_t*, hipStream_t);

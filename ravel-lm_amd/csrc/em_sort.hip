@@ -237,6 +237,340 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
   }
 }
 
+// ------------------------------------------------------------------------
+// Fused path.  pack_hist -> scan_hist -> scatter (pass 0, reduce-then-scan)
+// -> sweep (passes >= 1, decoupled look-back).  Used when the per-block LDS
+// budget below holds; the generic path above handles every other shape.
+
+constexpr int kPackThreads = 512;
+constexpr int kPackLdsBytes = 33 * 1024;  // keys of one pack tile, [CC][TT + 1]
+constexpr int kHistWords = 4096;          // CC * npass * 256 histogram words
+constexpr int kSweepItems = 16;           // keys per thread of a look-back sweep
+constexpr int kSweepTile = kSortThreads * kSweepItems;
+constexpr uint32_t kFlagA = 1u << 30;     // tile aggregate published
+constexpr uint32_t kFlagP = 2u << 30;     // inclusive prefix published
+constexpr uint32_t kValMask = (1u << 30) - 1;
+constexpr int kSpinLimit = 1 << 20;
+constexpr int kPackBatch = 16;            // address loads in flight per pack thread
+constexpr int kLookBatch = 16;            // predecessor tiles read per look-back round
+constexpr int kScatter0Items = 8;         // pass-0 scatter tile = 2048 keys
+
+// One block packs TT time steps of CC heads of one batch row: the [TT, CC]
+// slab of the [B,T,C] address tensor goes through LDS into segment-major keys,
+// with per-(segment, tile) histograms of every digit pass.  Sibling head
+// groups of one time tile are consecutive logical blocks, which xcd_block
+// places on one XCD, so the 128-byte address rows they share stay in one L2.
+template <typename U, typename AT>
+__global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
+    const AT* __restrict__ addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
+    int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int npass, int ntiles,
+    int64_t nlogical, U* __restrict__ keys, uint32_t* __restrict__ hist) {
+  __shared__ U tile[kPackLdsBytes / sizeof(U)];
+  __shared__ uint32_t h[kHistWords];
+  const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
+  if (logical >= nlogical) return;  // padding block of the XCD-rounded grid (uniform)
+  const int cg = (int)(logical % ncg);
+  const int64_t rest = logical / ncg;
+  const int tb = (int)(rest % ntiles);
+  const int64_t b = rest / ntiles;
+  const int c0 = cg * CC;
+  const int cc = (int)((C - c0) < CC ? (C - c0) : CC);
+  const int64_t t0 = (int64_t)tb * TT;
+  const int tt = (int)((T - t0) < TT ? (T - t0) : TT);
+  const int n = tt * cc;
+  const int pitch = TT + 1;
+  const int per = npass * kRadix;
+  const int hw = cc * per;
+  for (int i = threadIdx.x; i < hw; i += kPackThreads) h[i] = 0;
+  __syncthreads();
+  const AT* arow = addr + (b * T + t0) * C + c0;
+  for (int i0 = 0; i0 < n; i0 += kPackThreads * kPackBatch) {
+    AT av[kPackBatch];
+#pragma unroll
+    for (int j = 0; j < kPackBatch; ++j) {  // all loads first: one memory latency per batch
+      const int i = i0 + j * kPackThreads + threadIdx.x;
+      const int tl = i / cc;
+      av[j] = i < n ? arow[(int64_t)tl * C + (i - tl * cc)] : AT(0);
+    }
+#pragma unroll
+    for (int j = 0; j < kPackBatch; ++j) {
+      const int i = i0 + j * kPackThreads + threadIdx.x;
+      if (i < n) {
+        const int tl = i / cc;
+        const int cl = i - tl * cc;
+        int64_t a = reduce_addr((int64_t)av[j], A, mode, trunc32 != 0);
+        if (wmask && !wmask[b * T + t0 + tl]) a = A;
+        const U u = ((U)a << tbits) | (U)(t0 + tl);
+        tile[cl * pitch + tl] = u;
+        for (int p = 0; p < npass; ++p)
+          atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (tbits + 8 * p)) & (kRadix - 1))], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += kPackThreads) {
+    const int cl = i / tt;
+    const int tl = i - cl * tt;
+    keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
+  }
+  // hist layout [seg][tile][pass][256]: one contiguous npass KB run per head.
+  for (int i = threadIdx.x; i < hw; i += kPackThreads) {
+    const int cl = i / per;
+    const int r = i - cl * per;
+    hist[(((b * C + c0 + cl) * ntiles + tb) * (int64_t)per) + r] = h[i];
+  }
+}
+
+// Per segment: digit bases of every pass, and the pass-0 offsets of each
+// scatter tile (m consecutive pack tiles): offs[seg][tile][d] = count of digit d
+// in the segment's earlier scatter tiles.  Also resets the look-back tickets.
+__global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restrict__ hist,
+                                                        int ntiles, int m, int npass,
+                                                        uint32_t* __restrict__ offs, int nsct,
+                                                        uint32_t* __restrict__ binbase,
+                                                        uint32_t* __restrict__ tickets) {
+  constexpr int G = 1024 / kRadix;  // tile groups
+  constexpr int U8 = 8;
+  __shared__ uint32_t part[G][kRadix];
+  __shared__ uint32_t tmp[1024 / kWave + 1];
+  const int d = threadIdx.x % kRadix;
+  const int g = threadIdx.x / kRadix;
+  const int64_t seg = blockIdx.x;
+  const int per = npass * kRadix;
+  const uint32_t* hs = hist + seg * (int64_t)ntiles * per;
+  // group g owns whole scatter tiles [slo, shi), i.e. pack tiles [slo*m, shi*m)
+  const int slen = (nsct + G - 1) / G;
+  const int slo = g * slen < nsct ? g * slen : nsct;
+  const int shi = (slo + slen) < nsct ? (slo + slen) : nsct;
+  const int lo = slo * m;
+  const int hi = (shi * m) < ntiles ? (shi * m) : ntiles;
+  if (threadIdx.x < npass) tickets[(int64_t)threadIdx.x * gridDim.x + seg] = 0;  // [pass][seg]
+  if (seg == 0 && threadIdx.x == 0) tickets[(int64_t)npass * gridDim.x] = 0;   // error word
+  for (int p = 0; p < npass; ++p) {
+    uint32_t sum = 0;
+    for (int t0 = lo; t0 < hi; t0 += U8) {
+      uint32_t v[U8];
+#pragma unroll
+      for (int j = 0; j < U8; ++j) v[j] = (t0 + j < hi) ? hs[(int64_t)(t0 + j) * per + p * kRadix + d] : 0u;
+#pragma unroll
+      for (int j = 0; j < U8; ++j) sum += v[j];
+    }
+    part[g][d] = sum;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int q = 0; q < G; ++q) {
+      if (q < g) before += part[q][d];
+      total += part[q][d];
+    }
+    if (p == 0) {
+      uint32_t run = before;
+      for (int st = slo; st < shi; ++st) {
+        offs[((seg * nsct) + st) * kRadix + d] = run;
+        const int e = ((st + 1) * m) < ntiles ? ((st + 1) * m) : ntiles;
+        uint32_t v[U8];
+        int t = st * m;
+        for (; t < e; t += U8) {
+#pragma unroll
+          for (int j = 0; j < U8; ++j) v[j] = (t + j < e) ? hs[(int64_t)(t + j) * per + d] : 0u;
+#pragma unroll
+          for (int j = 0; j < U8; ++j) run += v[j];
+        }
+      }
+    }
+    __syncthreads();
+    // Every thread takes part in the block scan (it synchronizes); only group
+    // 0 contributes, so thread d of group 0 receives the sum over digits < d.
+    const uint32_t ex = block_excl_scan<1024>(g == 0 ? total : 0u, tmp, nullptr);
+    if (g == 0) binbase[(seg * npass + p) * kRadix + d] = ex;
+    __syncthreads();
+  }
+}
+
+// Stable wave-striped ranking of one tile, shared by the pass-0 scatter and the
+// look-back sweeps.  On return: key/rank per item, wcnt[w][d] = exclusive
+// offsets of digit d over the block's waves, dstart[d] = exclusive offset of
+// digit d inside the tile; the thread with tid == d gets the tile count in *own.
+template <typename U, int ITEMS>
+__device__ __forceinline__ void rank_tile(const U* __restrict__ src, int n, int shift,
+                                          uint32_t (*wcnt)[kRadix], uint32_t* dstart,
+                                          uint32_t* scan_tmp, U* key, uint32_t* rank,
+                                          uint32_t* own) {
+  constexpr int NW = kSortThreads / kWave;
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) wcnt[i][tid] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = w * kWave * ITEMS + i * kWave + lane;
+    key[i] = idx < n ? src[idx] : U(0);
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = w * kWave * ITEMS + i * kWave + lane;
+    const bool valid = idx < n;
+    const uint32_t d = (uint32_t)(key[i] >> shift) & (kRadix - 1);
+    const uint64_t peers = match_byte(d) & __ballot(valid);
+    uint32_t old = 0;
+    if (valid) old = wcnt[w][d];
+    __builtin_amdgcn_wave_barrier();
+    if (valid && lane == __ffsll((unsigned long long)peers) - 1)
+      wcnt[w][d] = old + (uint32_t)__popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    rank[i] = old + (uint32_t)__popcll(peers & lanemask_lt());
+  }
+  __syncthreads();
+  uint32_t tot = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const uint32_t c = wcnt[i][tid];
+    wcnt[i][tid] = tot;
+    tot += c;
+  }
+  *own = tot;
+  dstart[tid] = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
+}
+
+// Stage the ranked tile in LDS in local sorted order, then write each digit's
+// run to its global position (gbase[d] + local index), bounded by the segment.
+template <typename U, int ITEMS>
+__device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* rank, int n,
+                                                int shift, uint32_t (*wcnt)[kRadix],
+                                                const uint32_t* dstart, const int64_t* gbase,
+                                                U* stage, U* __restrict__ dst, int64_t T) {
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = w * kWave * ITEMS + i * kWave + lane;
+    if (idx < n) {
+      const uint32_t d = (uint32_t)(key[i] >> shift) & (kRadix - 1);
+      stage[dstart[d] + wcnt[w][d] + rank[i]] = key[i];
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < n; idx += kSortThreads) {
+    const U k = stage[idx];
+    const uint32_t d = (uint32_t)(k >> shift) & (kRadix - 1);
+    const int64_t pos = gbase[d] + idx;
+    if (pos >= 0 && pos < T) dst[pos] = k;
+  }
+}
+
+__device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t words) {
+  if (!p) return;
+  const int64_t per = (words + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = (int64_t)blockIdx.x * per;
+  const int64_t hi = (lo + per) < words ? (lo + per) : words;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) p[i] = 0;
+}
+
+template <typename U, int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
+    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
+    const uint32_t* __restrict__ binbase, int npass, int64_t T, int ntiles, int shift,
+    uint32_t* __restrict__ next_status, int64_t next_words) {
+  constexpr int NW = kSortThreads / kWave;
+  constexpr int TILE = kSortThreads * ITEMS;
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ int64_t gbase[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ U stage[TILE];
+  const int tid = threadIdx.x;
+  const int64_t seg = blockIdx.x / ntiles;
+  const int tile = (int)(blockIdx.x - seg * ntiles);
+  const int64_t start = (int64_t)tile * TILE;
+  const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  // Offsets first: their latency overlaps the key loads and the ranking.
+  const int64_t gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
+                       (int64_t)binbase[seg * npass * kRadix + tid];
+  U key[ITEMS];
+  uint32_t rank[ITEMS];
+  uint32_t own;
+  rank_tile<U, ITEMS>(in + seg * T + start, n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  gbase[tid] = gofs - (int64_t)dstart[tid];
+  __syncthreads();
+  stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
+  zero_slice(next_status, next_words);
+}
+
+template <typename U, int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void sweep_kernel(
+    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ binbase_p,
+    int npass, uint32_t* __restrict__ status, uint32_t* __restrict__ ticket, int64_t T,
+    int ntiles, int shift, uint32_t* __restrict__ next_status, int64_t next_words,
+    uint32_t* __restrict__ err) {
+  constexpr int NW = kSortThreads / kWave;
+  constexpr int TILE = kSortThreads * ITEMS;
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ int64_t gbase[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ uint32_t s_ticket;
+  __shared__ U stage[TILE];
+  // The segment comes from the block id; the tile within the segment from a
+  // per-segment ticket, so a tile only ever waits on tiles of its segment that
+  // running blocks already claimed.
+  const int tid = threadIdx.x;
+  const int64_t seg = blockIdx.x / ntiles;
+  if (tid == 0) s_ticket = atomicAdd(&ticket[seg], 1u);
+  __syncthreads();
+  const int tile = (int)s_ticket;
+  if (tile >= ntiles) return;  // uniform per block; tickets run 0..ntiles-1
+  const int64_t start = (int64_t)tile * TILE;
+  const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  const int64_t base_d = (int64_t)binbase_p[seg * npass * kRadix + tid];
+  U key[ITEMS];
+  uint32_t rank[ITEMS];
+  uint32_t own;
+  rank_tile<U, ITEMS>(in + seg * T + start, n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+
+  // Decoupled look-back over the earlier tiles of this segment, one digit per
+  // thread.  Up to kLookBatch predecessor words are read per round, so a
+  // tile whose predecessors already published costs one memory round trip.
+  uint32_t* st = status + (seg * ntiles) * (int64_t)kRadix;
+  __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], (tile == 0 ? kFlagP : kFlagA) | own,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t excl = 0;
+  bool ok = true;
+  bool done = tile == 0;
+  for (int hi = tile - 1; !done && hi >= 0; hi -= kLookBatch) {
+    uint32_t v[kLookBatch];
+#pragma unroll
+    for (int j = 0; j < kLookBatch; ++j)
+      v[j] = (hi - j >= 0) ? __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : kFlagP;
+#pragma unroll
+    for (int j = 0; j < kLookBatch; ++j) {
+      if (done || hi - j < 0) continue;
+      uint32_t w = v[j];
+      int spins = 0;
+      while ((w & ~kValMask) == 0 && spins < kSpinLimit) {
+        __builtin_amdgcn_s_sleep(1);
+        w = __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        ++spins;
+      }
+      if ((w & ~kValMask) == 0) {
+        ok = false;
+        done = true;
+        continue;
+      }
+      excl += w & kValMask;
+      if ((w & ~kValMask) == kFlagP) done = true;
+    }
+  }
+  if (!ok) atomicOr(err, 1u);
+  if (tile > 0)
+    __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kFlagP | ((excl + own) & kValMask),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  gbase[tid] = base_d + (int64_t)excl - (int64_t)dstart[tid];
+  __syncthreads();
+  stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
+  zero_slice(next_status, next_words);
+}
+
 int pack_tt(int64_t C, size_t key_bytes) {
   int tt = kPackTT;
   while (tt > 1 && (size_t)C * (size_t)(tt + 1) * key_bytes > 48 * 1024) tt >>= 1;
@@ -247,12 +581,121 @@ int pack_tt(int64_t C, size_t key_bytes) {
 
 size_t sort_counts_words(const Tape& tp) {
   const int64_t ntiles = (tp.T + kTile - 1) / kTile;
-  return (size_t)(tp.nseg() * kRadix * ntiles);
+  const size_t generic = (size_t)(tp.nseg() * kRadix * ntiles);
+  const size_t fused = tp.fused ? sort_fused_words(tp, tp.wide() ? 8 : 4) : 0;
+  return generic > fused ? generic : fused;
+}
+
+namespace {
+
+// Pack plan of the fused path: TT time steps x CC heads per pack block, or
+// TT == 0 when the fused path does not apply to this tape.
+struct PackPlan {
+  int TT = 0, CC = 0;
+};
+
+PackPlan fused_plan(const Tape& tp, size_t key_bytes) {
+  PackPlan pl;
+  const int npass = (tp.abits + 7) / 8;
+  if (npass < 1 || tp.T >= ((int64_t)1 << 30)) return pl;
+  int tt = kSortThreads * kScatter0Items;  // a pack tile divides the 2048-key scatter tile
+  while (tt > 64 && tt / 2 >= tp.T) tt >>= 1;  // short tapes: smaller pack tiles
+  const int64_t cap = (int64_t)(kPackLdsBytes / key_bytes);
+  int64_t cc = cap / (tt + 1);
+  if (cc > tp.C) cc = tp.C;
+  if (cc * npass * kRadix > kHistWords) cc = kHistWords / (npass * kRadix);
+  if (cc < 1) return pl;
+  pl.TT = tt;
+  pl.CC = (int)cc;
+  return pl;
+}
+
+int64_t sweep_tiles(const Tape& tp) { return (tp.T + kSweepTile - 1) / kSweepTile; }
+
+}  // namespace
+
+int64_t scatter0_tiles(const Tape& tp) {
+  constexpr int kT = kSortThreads * kScatter0Items;
+  return (tp.T + kT - 1) / kT;
+}
+
+size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
+  const int tt = fused_plan(tp, key_bytes).TT;
+  if (!tt) return 0;
+  const int npass = (tp.abits + 7) / 8;
+  const int64_t nt0 = (tp.T + tt - 1) / tt;
+  const int64_t hist = tp.nseg() * nt0 * npass * kRadix;
+  const int64_t offs = tp.nseg() * scatter0_tiles(tp) * kRadix;
+  const int64_t bins = tp.nseg() * npass * kRadix;
+  const int64_t status = tp.nseg() * sweep_tiles(tp) * kRadix;
+  return (size_t)(hist + offs + bins + 2 * status + (npass + 1) * tp.nseg());
+}
+
+template <typename U>
+static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* wmask,
+                                  const Tape& tp, PackPlan pl, U* ka, U* kb, uint32_t* words,
+                                  U** sorted, hipStream_t s) {
+  const int tt = pl.TT;
+  const int ncg = (int)((tp.C + pl.CC - 1) / pl.CC);
+  const int npass = (tp.abits + 7) / 8;
+  const int nt0 = (int)((tp.T + tt - 1) / tt);
+  const int nsct = (int)scatter0_tiles(tp);
+  const int m = (kSortThreads * kScatter0Items) / tt;  // pack tiles per scatter tile
+  const int64_t hist_words = tp.nseg() * nt0 * npass * kRadix;
+  const int64_t offs_words = tp.nseg() * nsct * kRadix;
+  const int64_t bin_words = tp.nseg() * npass * kRadix;
+  const int nts = (int)sweep_tiles(tp);
+  const int64_t status_words = tp.nseg() * nts * kRadix;
+  uint32_t* hist = words;
+  uint32_t* offs = hist + hist_words;
+  uint32_t* binbase = offs + offs_words;
+  uint32_t* status[2] = {binbase + bin_words, binbase + bin_words + status_words};
+  uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then the error word
+  uint32_t* err = tickets + (int64_t)npass * tp.nseg();
+  const int64_t nlogical = tp.B * nt0 * ncg;
+  const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
+  if (addr64)
+    pack_hist_kernel<U, int64_t><<<pgrid, kPackThreads, 0, s>>>(
+        (const int64_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
+        pl.CC, ncg, npass, nt0, nlogical, ka, hist);
+  else
+    pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
+        (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
+        pl.CC, ncg, npass, nt0, nlogical, ka, hist);
+  scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, npass, offs, nsct, binbase,
+                                                         tickets);
+  const unsigned g0 = (unsigned)(tp.nseg() * nsct);
+  uint32_t* next0 = npass > 1 ? status[0] : nullptr;
+  scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(ka, kb, offs, binbase, npass, tp.T,
+                                                                 nsct, tp.tbits, next0,
+                                                                 status_words);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  U* cur = kb;
+  U* alt = ka;
+  const unsigned gs = (unsigned)(tp.nseg() * nts);
+  for (int p = 1; p < npass; ++p) {
+    uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
+    sweep_kernel<U, kSweepItems><<<gs, kSortThreads, 0, s>>>(
+        cur, alt, binbase + p * kRadix, npass, status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts,
+        tp.tbits + 8 * p, next, status_words, err);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    U* t = cur;
+    cur = alt;
+    alt = t;
+  }
+  *sorted = cur;
+  return hipSuccess;
 }
 
 template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp, U* ka,
                      U* kb, uint32_t* counts, U** sorted, hipStream_t s) {
+  if (tp.fused) {
+    const PackPlan pl = fused_plan(tp, sizeof(U));
+    if (pl.TT) return sort_tape_fused<U>(addr, addr64, wmask, tp, pl, ka, kb, counts, sorted, s);
+  }
   const int tt = pack_tt(tp.C, sizeof(U));
   const size_t shm = (size_t)tp.C * (tt + 1) * sizeof(U);
   const int64_t ntb = (tp.T + tt - 1) / tt;

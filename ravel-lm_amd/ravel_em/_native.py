@@ -34,6 +34,9 @@ SIGNATURES = {
     "ravel_em_last_error": (ctypes.c_char_p, []),
     "ravel_em_abi_version": (_i, []),
     "ravel_em_key_bits": (_i, [_i64, _i64, _i64, _i64]),
+    "ravel_em_set_sort_path": (_i, [_i]),
+    "ravel_em_profile_start": (_i, []),
+    "ravel_em_profile_stop": (_i, [_vp, _vp, _i]),
     "ravel_em_sort_order_workspace": (_sz, [_i64, _i64, _i64, _i64, _i]),
     "ravel_em_sort_order": (_i, [_vp, _i, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ravel_em_latest_k_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i, _i]),

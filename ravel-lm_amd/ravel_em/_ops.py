@@ -208,6 +208,8 @@ def sort_order(write_addresses: Tensor, write_mask: Optional[Tensor], address_sp
     n_valid = B * T * C if write_mask is None else C * int(write_mask.sum().item())
     keys = torch.empty(n_valid, dtype=key_dtype, device=dev)
     order = torch.empty(n_valid, dtype=torch.int64, device=dev)
+    if n_valid == 0:
+        return keys, order
     nbytes = lib.ravel_em_sort_order_workspace(B, T, C, address_space, int(write_mask is not None))
     ws = nat.workspace(nbytes, dev)
     _call(

@@ -113,6 +113,9 @@ SMALL = [
     (1, 70000, 1, 2, None, None, True, False, 3),  # long runs across many tiles
     (2, 3000, 3, 1 << 21, None, None, False, True, 2),  # 64-bit packed keys (21+12 bits)
     (2, 257, 5, 100003, None, None, True, True, 1),  # odd sizes, 3 digit passes
+    (1, 3000, 40, 1 << 20, None, None, False, False, 2),  # 3 passes x 40 heads: generic sort
+    (1, 300, 200, 50, None, None, False, True, 1),  # 200 heads: pack tile over the LDS budget
+    (2, 9000, 3, 1 << 17, None, None, True, False, 2),  # masked, 3 passes, 2 look-back sweeps
 ]
 
 
@@ -199,3 +202,74 @@ def test_baseline_config_parity(device, name):
         okeys, oorder = oracle.sort_order(w.write, address_space=w.address_space)
         assert np.array_equal(keys.cpu().numpy().astype(np.int64), okeys)
         assert np.array_equal(order.cpu().numpy(), oorder)
+
+
+def test_resolve_and_gather_stage_entry_points(device):
+    """ravel_em_latest_k_resolve + ravel_em_gather_rows reproduce the fused call."""
+    from ravel_em import _native as nat
+
+    lib = nat.library()
+    for sep, masked in [(False, False), (True, False), (False, True)]:
+        g = torch.Generator().manual_seed(int(sep) * 2 + int(masked))
+        B, T, C, A, D, k = 2, 700, 3, 23, 12, 3
+        w = torch.randint(0, A, (B, T, C), generator=g).to(device)
+        r = torch.randint(0, A, (B, T, C), generator=g).to(device) if sep else None
+        m = (torch.rand(B, T, generator=g) < 0.5).to(device) if masked else None
+        p = torch.randn(B, T, C, D, generator=g).to(device, torch.bfloat16)
+        src = torch.empty(B, T, C, k, dtype=torch.int32, device=device)
+        ws = nat.workspace(lib.ravel_em_latest_k_resolve_workspace(B, T, C, A, k, int(sep), int(masked)), device)
+        stream = torch.cuda.current_stream(device).cuda_stream
+        nat.check(lib.ravel_em_latest_k_resolve(w.data_ptr(), None if r is None else r.data_ptr(), nat.INT64,
+                                                None if m is None else m.data_ptr(), B, T, C, A, k,
+                                                src.data_ptr(), ws.data_ptr(), ws.numel(), stream))
+        vals = torch.empty(B, T, C, k, D, dtype=torch.bfloat16, device=device)
+        mask = torch.empty(B, T, C, k, dtype=torch.bool, device=device)
+        nat.check(lib.ravel_em_gather_rows(p.data_ptr(), B * T * C, D * 2, src.data_ptr(), B * T * C * k,
+                                           vals.data_ptr(), mask.data_ptr(), stream))
+        want_v, want_m, want_s = causal_last_k_sources(w, p, r, address_space=A, k=k, write_mask=m)
+        assert torch.equal(src, want_s) and torch.equal(vals, want_v) and torch.equal(mask, want_m)
+        osrc = oracle.latest_k_src(w, r, address_space=A, k=k, write_mask=m)
+        assert np.array_equal(src.cpu().numpy(), osrc)
+
+
+def test_stage_timer_reports_each_stage(device):
+    import ctypes
+
+    from ravel_em import _native as nat
+
+    lib = nat.library()
+    w = torch.randint(0, 50, (2, 4000, 4), device=device)
+    p = torch.randn(2, 4000, 4, 8, device=device)
+    nat.check(lib.ravel_em_profile_start())
+    for _ in range(3):
+        causal_last_k_lookup(w, p, address_space=50, k=2)
+    ms = (ctypes.c_double * 5)()
+    calls = (ctypes.c_int * 5)()
+    nat.check(lib.ravel_em_profile_stop(ms, calls, 5))
+    assert list(calls)[:3] == [3, 3, 3] and all(ms[i] > 0 for i in range(3))
+    causal_last_k_lookup(w, p, address_space=50, k=2)  # timer off again: nothing recorded
+    nat.check(lib.ravel_em_profile_stop(ms, calls, 5))
+    assert list(calls) == [0] * 5
+
+
+@pytest.mark.parametrize("shape", [(4, 65536, 16, 65536, False), (2, 5000, 3, 300, True), (3, 2000, 8, 1 << 20, False),
+                                   (1, 70000, 2, 3, True)])
+def test_fused_and_generic_sorts_agree(device, shape):
+    from ravel_em import _native as nat
+
+    B, T, C, A, masked = shape
+    g = torch.Generator().manual_seed(T)
+    w = torch.randint(0, A, (B, T, C), generator=g).to(device)
+    m = (torch.rand(B, T, generator=g) < 0.5).to(device) if masked else None
+    lib = nat.library()
+    outs = []
+    for path in (0, 1):
+        nat.check(lib.ravel_em_set_sort_path(path))
+        try:
+            outs.append(sort_order(w, address_space=A, write_mask=m))
+        finally:
+            nat.check(lib.ravel_em_set_sort_path(0))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    if B * T * C <= 1 << 20:
+        okeys, oorder = oracle.sort_order(w, address_space=A, write_mask=m)
+        assert np.array_equal(outs[0][1].cpu().numpy(), oorder)
