@@ -58,6 +58,101 @@ __global__ __launch_bounds__(256) void link_same_kernel(const U* __restrict__ so
   }
 }
 
+// read == write, k == 1, short segments.  One block per (segment, time chunk)
+// streams the whole sorted segment from L2 with 16-byte vector loads (many in
+// flight per CU), keeps the records whose time falls in its chunk and writes
+// their source into LDS at (t - chunk start); the chunk of src_seg then goes
+// out with coalesced stores.  The random scatter thus happens in LDS instead
+// of as 4-byte global writes.  A key's predecessor in sorted order is the
+// previous key of the same thread's vector, else the last key of the previous
+// lane (shuffle), of the previous wave (LDS exchange) or of the previous row.
+constexpr int kLinkThreads = 1024;
+constexpr int kLinkWaves = kLinkThreads / kWave;
+constexpr int kLinkLdsWords = 16384;  // 64 KiB of int32 source slots = the time chunk
+constexpr int kLinkRows = 8;          // vector rows per thread per round
+
+template <typename U>
+__device__ __forceinline__ U shfl_up1(U x) {
+  if (sizeof(U) == 4) return (U)__shfl_up((int)(uint32_t)x, 1, kWave);
+  const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)x, 1, kWave);
+  const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)((uint64_t)x >> 32), 1, kWave);
+  return (U)(((uint64_t)hi << 32) | lo);
+}
+
+template <typename U>
+__global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __restrict__ sorted,
+                                                                int64_t T, int64_t C, int tbits,
+                                                                int64_t chunk, int nchunk,
+                                                                int64_t nseg,
+                                                                int32_t* __restrict__ src_seg) {
+  constexpr int VEC = 16 / sizeof(U);  // keys per 16-byte load
+  constexpr int ROWKEYS = kLinkThreads * VEC;
+  constexpr int ROUND = kLinkRows * ROWKEYS;
+  typedef U vec_t __attribute__((ext_vector_type(VEC)));
+  __shared__ int32_t buf[kLinkLdsWords];
+  __shared__ U xch[2][kLinkRows][kLinkWaves];  // last key of each wave's part of a row
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const int64_t logical = xcd_block(blockIdx.x, gridDim.x);  // chunks of a segment share an XCD
+  const int64_t seg = logical / nchunk;
+  const int ch = (int)(logical - seg * nchunk);
+  const bool live = seg < nseg;  // the grid is rounded up to a multiple of the XCD count
+  const int64_t t_lo = (int64_t)ch * chunk;
+  const int64_t t_hi = (t_lo + chunk) < T ? (t_lo + chunk) : T;
+  const int nslot = live && t_hi > t_lo ? (int)(t_hi - t_lo) : 0;
+  for (int i = tid; i < nslot; i += kLinkThreads) buf[i] = -1;
+  const int64_t b = seg / C;
+  const int64_t c = seg - b * C;
+  const U* sk = sorted + (live ? seg : 0) * T;
+  const int64_t nround = nslot > 0 ? (T + ROUND - 1) / ROUND : 0;
+  const bool aligned = (T % VEC) == 0;  // vector loads need T*sizeof(U) 16-byte aligned rows
+  for (int64_t r0 = 0; r0 < nround; ++r0) {
+    const int64_t base = r0 * ROUND;
+    const int xb = (int)(r0 & 1);
+    U v[kLinkRows][VEC];
+#pragma unroll
+    for (int r = 0; r < kLinkRows; ++r) {
+      const int64_t p = base + (int64_t)r * ROWKEYS + (int64_t)tid * VEC;
+      if (aligned && p + VEC <= T) {
+        const vec_t x = *(const vec_t*)(sk + p);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[r][e] = x[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[r][e] = (p + e < T) ? sk[p + e] : U(0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kLinkRows; ++r)
+      if (lane == kWave - 1) xch[xb][r][w] = v[r][VEC - 1];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kLinkRows; ++r) {
+      const int64_t p0 = base + (int64_t)r * ROWKEYS + (int64_t)tid * VEC;
+      U prev = shfl_up1(v[r][VEC - 1]);
+      if (lane == 0) {
+        if (w > 0) prev = xch[xb][r][w - 1];
+        else if (r > 0) prev = xch[xb][r - 1][kLinkWaves - 1];
+        else prev = xch[xb ^ 1][kLinkRows - 1][kLinkWaves - 1];  // previous round (unused at p = 0)
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t p = p0 + e;
+        const U u = v[r][e];
+        const U pk = e > 0 ? v[r][e - 1] : prev;
+        const int64_t t = (int64_t)(u & tmask);
+        if (p < T && p > 0 && t >= t_lo && t < t_hi && (pk >> tbits) == (u >> tbits) &&
+            (int64_t)(pk & tmask) < T)
+          buf[t - t_lo] = (int32_t)((b * T + (int64_t)(pk & tmask)) * C + c);
+      }
+    }
+    __syncthreads();  // xch[xb ^ 1] is rewritten next round
+  }
+  __syncthreads();
+  int32_t* dst = src_seg + (live ? seg : 0) * T + t_lo;
+  for (int i = tid; i < nslot; i += kLinkThreads) dst[i] = buf[i];
+}
+
 template <typename U, typename AT>
 __global__ __launch_bounds__(256) void search_reads_kernel(
     const U* __restrict__ sorted, const AT* __restrict__ raddr, int64_t N, int64_t T, int64_t C,
@@ -109,8 +204,9 @@ __global__ __launch_bounds__(256) void search_reads_kernel(
 }
 
 // Each block copies a contiguous run of row units; every thread keeps kIlp
-// independent 16-byte loads in flight.  SEG selects a segment-major src.
-constexpr int kIlp = 4;
+// independent 16-byte loads in flight (2 measured best at cfg4, against 1, 4
+// and 8).  SEG selects a segment-major src.
+constexpr int kIlp = 2;
 
 template <typename V, int SHIFT, bool SEG>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ rows,
@@ -121,7 +217,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
                                                          uint8_t* __restrict__ mask,
                                                          int32_t* __restrict__ src_out) {
   const int64_t total = nrows * upr;
-  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t lb = blockIdx.x;  // plain order: spreads each XCD's writes over the output
   const int64_t step = (int64_t)gridDim.x * blockDim.x * kIlp;
   for (int64_t base = lb * blockDim.x * kIlp + threadIdx.x; base < total; base += step) {
     int32_t s[kIlp];
@@ -261,6 +357,13 @@ hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s) {
 template <typename U>
 hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s) {
   const int64_t N = tp.n();
+  const int64_t nchunk = (tp.T + kLinkLdsWords - 1) / kLinkLdsWords;
+  if (k == 1 && nchunk >= 1 && nchunk <= 8) {  // segment read amplification <= 8x
+    const unsigned grid = xcd_grid(tp.nseg() * nchunk, 1, (int64_t)1 << 31);
+    link1_lds_kernel<U><<<grid, kLinkThreads, 0, s>>>(sorted, tp.T, tp.C, tp.tbits, kLinkLdsWords,
+                                                      (int)nchunk, tp.nseg(), src_seg);
+    return hipGetLastError();
+  }
   link_same_kernel<U><<<xcd_grid(N, 256), 256, 0, s>>>(sorted, N, tp.T, k, src_seg, tp.tbits, tp.C);
   return hipGetLastError();
 }

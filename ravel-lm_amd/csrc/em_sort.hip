@@ -391,20 +391,25 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restr
 // offsets of digit d over the block's waves, dstart[d] = exclusive offset of
 // digit d inside the tile; the thread with tid == d gets the tile count in *own.
 template <typename U, int ITEMS>
-__device__ __forceinline__ void rank_tile(const U* __restrict__ src, int n, int shift,
-                                          uint32_t (*wcnt)[kRadix], uint32_t* dstart,
-                                          uint32_t* scan_tmp, U* key, uint32_t* rank,
-                                          uint32_t* own) {
-  constexpr int NW = kSortThreads / kWave;
+__device__ __forceinline__ void load_tile(const U* __restrict__ src, int n, U* key) {
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) wcnt[i][tid] = 0;
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int idx = w * kWave * ITEMS + i * kWave + lane;
     key[i] = idx < n ? src[idx] : U(0);
   }
+}
+
+// Keys must come from load_tile (wave-striped ownership).
+template <typename U, int ITEMS>
+__device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRadix],
+                                          uint32_t* dstart, uint32_t* scan_tmp, const U* key,
+                                          uint32_t* rank, uint32_t* own) {
+  constexpr int NW = kSortThreads / kWave;
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) wcnt[i][tid] = 0;
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int idx = w * kWave * ITEMS + i * kWave + lane;
@@ -456,6 +461,31 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
   }
 }
 
+// Tile prefix and digit base of one pass, read straight from the pack
+// histograms of the segment (used when a segment has few pack tiles): thread
+// d returns sum_{j < upto} hist[j][pass][d] + (exclusive scan over digits of
+// sum_j hist[j][pass][d]).  All threads must call it (it synchronizes).
+constexpr int kDirectMaxTiles = 64;
+
+__device__ __forceinline__ int64_t direct_offset(const uint32_t* __restrict__ hs, int nt0, int per,
+                                                 int pass, int upto, uint32_t* scan_tmp) {
+  const int d = threadIdx.x;
+  uint32_t pre = 0, tot = 0;
+  for (int j0 = 0; j0 < nt0; j0 += 16) {
+    uint32_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      v[j] = (j0 + j < nt0) ? hs[(int64_t)(j0 + j) * per + pass * kRadix + d] : 0u;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      tot += v[j];
+      if (j0 + j < upto) pre += v[j];
+    }
+  }
+  const uint32_t base = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
+  return (int64_t)pre + (int64_t)base;
+}
+
 __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t words) {
   if (!p) return;
   const int64_t per = (words + gridDim.x - 1) / gridDim.x;
@@ -466,9 +496,10 @@ __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t wor
 
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
-    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
-    const uint32_t* __restrict__ binbase, int npass, int64_t T, int ntiles, int shift,
-    uint32_t* __restrict__ next_status, int64_t next_words) {
+    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ hist, int nt0,
+    int m, const uint32_t* __restrict__ offs, const uint32_t* __restrict__ binbase, int npass,
+    int64_t T, int ntiles, int64_t nblk, int shift, uint32_t* __restrict__ zero0, int64_t zero0_words,
+    uint32_t* __restrict__ zero1, int64_t zero1_words) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
@@ -476,29 +507,40 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   __shared__ int64_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ U stage[TILE];
+  zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
+  zero_slice(zero1, zero1_words);
   const int tid = threadIdx.x;
-  const int64_t seg = blockIdx.x / ntiles;
-  const int tile = (int)(blockIdx.x - seg * ntiles);
+  // Consecutive tiles of a segment on one XCD: their partial output lines merge in one L2.
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  const int64_t seg = lb / ntiles;
+  const int tile = (int)(lb - seg * ntiles);
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  // Offsets first: their latency overlaps the key loads and the ranking.
-  const int64_t gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
-                       (int64_t)binbase[seg * npass * kRadix + tid];
+  const int per = npass * kRadix;
+  int64_t gofs;
+  if (offs) {  // offsets from the scan kernel
+    gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
+           (int64_t)binbase[seg * npass * kRadix + tid];
+  } else {
+    gofs = direct_offset(hist + seg * (int64_t)nt0 * per, nt0, per, 0, tile * m, scan_tmp);
+  }
   U key[ITEMS];
+  load_tile<U, ITEMS>(in + seg * T + start, n, key);
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(in + seg * T + start, n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
   gbase[tid] = gofs - (int64_t)dstart[tid];
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
-  zero_slice(next_status, next_words);
 }
 
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ binbase_p,
-    int npass, uint32_t* __restrict__ status, uint32_t* __restrict__ ticket, int64_t T,
-    int ntiles, int shift, uint32_t* __restrict__ next_status, int64_t next_words,
+    const uint32_t* __restrict__ hist, int nt0, int pass, int npass,
+    uint32_t* __restrict__ status, uint32_t* __restrict__ ticket, int64_t T, int ntiles,
+    int64_t nblk, int shift, uint32_t* __restrict__ next_status, int64_t next_words,
     uint32_t* __restrict__ err) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
@@ -508,22 +550,29 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ uint32_t s_ticket;
   __shared__ U stage[TILE];
-  // The segment comes from the block id; the tile within the segment from a
-  // per-segment ticket, so a tile only ever waits on tiles of its segment that
-  // running blocks already claimed.
+  zero_slice(next_status, next_words);  // state of the next pass; every block, padding included
+  // The segment comes from the (XCD-local) block id; the tile within the
+  // segment from a per-segment ticket, so a tile only ever waits on tiles of
+  // its segment that running blocks already claimed.
   const int tid = threadIdx.x;
-  const int64_t seg = blockIdx.x / ntiles;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  const int64_t seg = lb / ntiles;
   if (tid == 0) s_ticket = atomicAdd(&ticket[seg], 1u);
   __syncthreads();
   const int tile = (int)s_ticket;
   if (tile >= ntiles) return;  // uniform per block; tickets run 0..ntiles-1
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  const int64_t base_d = (int64_t)binbase_p[seg * npass * kRadix + tid];
+  const int64_t base_d =
+      binbase_p ? (int64_t)binbase_p[seg * npass * kRadix + tid]
+                : direct_offset(hist + seg * (int64_t)nt0 * npass * kRadix, nt0, npass * kRadix,
+                                pass, 0, scan_tmp);
   U key[ITEMS];
+  load_tile<U, ITEMS>(in + seg * T + start, n, key);
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(in + seg * T + start, n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
 
   // Decoupled look-back over the earlier tiles of this segment, one digit per
   // thread.  Up to kLookBatch predecessor words are read per round, so a
@@ -568,7 +617,6 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   gbase[tid] = base_d + (int64_t)excl - (int64_t)dstart[tid];
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
-  zero_slice(next_status, next_words);
 }
 
 int pack_tt(int64_t C, size_t key_bytes) {
@@ -662,23 +710,31 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
     pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
         pl.CC, ncg, npass, nt0, nlogical, ka, hist);
-  scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, npass, offs, nsct, binbase,
-                                                         tickets);
-  const unsigned g0 = (unsigned)(tp.nseg() * nsct);
+  // Few pack tiles per segment: scatter and sweep blocks sum the histograms
+  // themselves; otherwise one scan kernel prepares offsets and digit bases.
+  const bool direct = nt0 <= kDirectMaxTiles;
+  const int64_t ticket_words = (int64_t)(npass + 1) * tp.nseg();  // [pass][seg] + error word
+  if (!direct)
+    scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, npass, offs, nsct, binbase,
+                                                           tickets);
+  const int64_t nblk0 = tp.nseg() * nsct;
+  const unsigned g0 = xcd_grid(nblk0, 1, (int64_t)1 << 31);
   uint32_t* next0 = npass > 1 ? status[0] : nullptr;
-  scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(ka, kb, offs, binbase, npass, tp.T,
-                                                                 nsct, tp.tbits, next0,
-                                                                 status_words);
+  scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
+      ka, kb, hist, nt0, m, direct ? nullptr : offs, binbase, npass, tp.T, nsct, nblk0, tp.tbits,
+      next0, status_words, direct ? tickets : nullptr, ticket_words);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   U* cur = kb;
   U* alt = ka;
-  const unsigned gs = (unsigned)(tp.nseg() * nts);
+  const int64_t nblks = tp.nseg() * nts;
+  const unsigned gs = xcd_grid(nblks, 1, (int64_t)1 << 31);
   for (int p = 1; p < npass; ++p) {
     uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
     sweep_kernel<U, kSweepItems><<<gs, kSortThreads, 0, s>>>(
-        cur, alt, binbase + p * kRadix, npass, status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts,
-        tp.tbits + 8 * p, next, status_words, err);
+        cur, alt, direct ? nullptr : binbase + p * kRadix, hist, nt0, p, npass,
+        status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts, nblks, tp.tbits + 8 * p, next,
+        status_words, err);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     U* t = cur;
