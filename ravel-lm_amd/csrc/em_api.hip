@@ -142,7 +142,10 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
   const bool link = !raddr && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
-  int32_t* src = (link || !out_src) ? bp.take<int32_t>((size_t)(tp.n() * k)) : out_src;
+  // The link writes segment-major sources (src_seg), which one tiled
+  // transpose turns record-major; the read search writes them record-major.
+  int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
+  int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
@@ -150,17 +153,16 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   stage_begin(kStageResolve, s);
-  if (link)
-    e = link_same<U>(sorted, tp, (int)k, src, s);
-  else
+  if (link) {
+    e = link_same<U>(sorted, tp, (int)k, src_seg, s);
+    if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
+  } else {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+  }
   stage_end(kStageResolve, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
   stage_begin(kStageGather, s);
-  if (link)
-    e = gather_rows_segmajor(payload, src, tp, (int)k, row_bytes, out_values, out_mask, out_src, s);
-  else
-    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
   stage_end(kStageGather, s);
   if (e != hipSuccess) return hip_fail(e, "gather");
   return RAVEL_EM_OK;
@@ -172,14 +174,14 @@ int resolve_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
   const bool link = !raddr && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
-  int32_t* src_seg = link ? bp.take<int32_t>((size_t)(tp.n() * k)) : nullptr;
+  int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (link) {
     e = link_same<U>(sorted, tp, (int)k, src_seg, s);
-    if (e == hipSuccess) e = src_record_major(src_seg, tp, (int)k, src, s);
+    if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
   }
@@ -191,7 +193,8 @@ template <typename U>
 size_t latest_k_ws_t(const Tape& tp, int64_t k, bool link, bool want_src) {
   Bump bp(nullptr);
   take_sort<U>(bp, tp);
-  if (link || !want_src) bp.take<int32_t>((size_t)(tp.n() * k));
+  if (!want_src) bp.take<int32_t>((size_t)(tp.n() * k));
+  if (link && tp.C > 1) bp.take<int32_t>((size_t)(tp.n() * k));
   return bp.off;
 }
 
@@ -461,7 +464,7 @@ size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int6
   const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
   Bump bp(nullptr);
   bp.off = sort_bytes(tp);
-  if (!has_read && !has_mask) bp.take<int32_t>((size_t)(tp.n() * k));
+  if (!has_read && !has_mask && C > 1) bp.take<int32_t>((size_t)(tp.n() * k));
   return bp.off;
 }
 

@@ -54,11 +54,17 @@ constexpr int kXcds = 8;
 __device__ __forceinline__ uint32_t xcd_block(uint32_t bid, uint32_t nblk) {
   return (bid % kXcds) * (nblk / kXcds) + bid / kXcds;
 }
-inline unsigned xcd_grid(int64_t work, int block, int64_t cap = 1 << 20) {
+// Groups of G consecutive logical blocks on one XCD, successive groups on
+// successive XCDs (the grid must be a multiple of kXcds * G).
+__device__ __forceinline__ uint32_t xcd_group_block(uint32_t bid, uint32_t G) {
+  const uint32_t x = bid % kXcds, q = bid / kXcds;
+  return (q / G) * (kXcds * G) + x * G + q % G;
+}
+inline unsigned xcd_grid(int64_t work, int block, int64_t cap = 1 << 20, int mult = kXcds) {
   int64_t g = (work + block - 1) / block;
   if (g > cap) g = cap;
-  g = (g + kXcds - 1) / kXcds * kXcds;
-  return (unsigned)(g < kXcds ? kXcds : g);
+  g = (g + mult - 1) / mult * mult;
+  return (unsigned)(g < mult ? mult : g);
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
@@ -137,7 +143,8 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
                       void* out_keys, bool keys64, int64_t* out_order, hipStream_t s);
 
 // Latest-k source indices, int32, -1 for a missing slot.  link_same writes them
-// segment-major ([B,C,T,k]); search_reads writes record-major ([B,T,C,k]).
+// segment-major ([B,C,T,k], the record-major layout when C == 1);
+// search_reads writes record-major ([B,T,C,k]).
 template <typename U>
 hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s);
 template <typename U>
@@ -147,11 +154,7 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
 // out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s);
-// Same, with src segment-major ([B,C,T,k]) and out/mask record-major; src_out
-// (optional) receives the sources record-major.
-hipError_t gather_rows_segmajor(const void* rows, const int32_t* src_seg, const Tape& tp, int k,
-                                int64_t row_bytes, void* out, uint8_t* mask, int32_t* src_out,
-                                hipStream_t s);
+// Segment-major sources -> record-major (a no-op layout change when C == 1).
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
                             hipStream_t s);
 // Opt-in per-stage timing (host side): brackets each stage with HIP events on

@@ -15,6 +15,8 @@
 //               16-byte vector loads and writes values + mask with coalesced
 //               non-temporal stores.  Only valid slots touch the payload.
 
+#include <algorithm>
+
 #include "em_common.h"
 
 namespace rem {
@@ -61,8 +63,8 @@ __global__ __launch_bounds__(256) void link_same_kernel(const U* __restrict__ so
 // read == write, k == 1, short segments.  One block per (segment, time chunk)
 // streams the whole sorted segment from L2 with 16-byte vector loads (many in
 // flight per CU), keeps the records whose time falls in its chunk and writes
-// their source into LDS at (t - chunk start); the chunk of src_seg then goes
-// out with coalesced stores.  The random scatter thus happens in LDS instead
+// their source into LDS at (t - chunk start); the chunk then goes out
+// segment-major ([B,C,T]) with coalesced stores.  The random scatter thus happens in LDS instead
 // of as 4-byte global writes.  A key's predecessor in sorted order is the
 // previous key of the same thread's vector, else the last key of the previous
 // lane (shuffle), of the previous wave (LDS exchange) or of the previous row.
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
                                                                 int64_t T, int64_t C, int tbits,
                                                                 int64_t chunk, int nchunk,
                                                                 int64_t nseg,
-                                                                int32_t* __restrict__ src_seg) {
+                                                                int32_t* __restrict__ src) {
   constexpr int VEC = 16 / sizeof(U);  // keys per 16-byte load
   constexpr int ROWKEYS = kLinkThreads * VEC;
   constexpr int ROUND = kLinkRows * ROWKEYS;
@@ -96,13 +98,13 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);  // chunks of a segment share an XCD
   const int64_t seg = logical / nchunk;
   const int ch = (int)(logical - seg * nchunk);
+  const int64_t b = seg / C;
+  const int64_t c = seg - b * C;
   const bool live = seg < nseg;  // the grid is rounded up to a multiple of the XCD count
   const int64_t t_lo = (int64_t)ch * chunk;
   const int64_t t_hi = (t_lo + chunk) < T ? (t_lo + chunk) : T;
   const int nslot = live && t_hi > t_lo ? (int)(t_hi - t_lo) : 0;
   for (int i = tid; i < nslot; i += kLinkThreads) buf[i] = -1;
-  const int64_t b = seg / C;
-  const int64_t c = seg - b * C;
   const U* sk = sorted + (live ? seg : 0) * T;
   const int64_t nround = nslot > 0 ? (T + ROUND - 1) / ROUND : 0;
   const bool aligned = (T % VEC) == 0;  // vector loads need T*sizeof(U) 16-byte aligned rows
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
     __syncthreads();  // xch[xb ^ 1] is rewritten next round
   }
   __syncthreads();
-  int32_t* dst = src_seg + (live ? seg : 0) * T + t_lo;
+  int32_t* dst = src + (live ? seg : 0) * T + t_lo;
   for (int i = tid; i < nslot; i += kLinkThreads) dst[i] = buf[i];
 }
 
@@ -203,21 +205,20 @@ __global__ __launch_bounds__(256) void search_reads_kernel(
   }
 }
 
-// Each block copies a contiguous run of row units; every thread keeps kIlp
-// independent 16-byte loads in flight (2 measured best at cfg4, against 1, 4
-// and 8).  SEG selects a segment-major src.
+// Each thread keeps kIlp independent 16-byte loads in flight (2 measured best
+// at cfg4, against 1, 4 and 8).  src is read once, in order; blocks run in
+// hardware order, which deals consecutive blocks to different XCDs and spreads
+// the output writes over all eight L2s.
 constexpr int kIlp = 2;
 
-template <typename V, int SHIFT, bool SEG>
+template <typename V, int SHIFT>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ rows,
                                                          const int32_t* __restrict__ src,
                                                          int64_t nrows, int upr, int64_t nsrc,
-                                                         int64_t T, int64_t C, int k,
                                                          V* __restrict__ out,
-                                                         uint8_t* __restrict__ mask,
-                                                         int32_t* __restrict__ src_out) {
+                                                         uint8_t* __restrict__ mask) {
   const int64_t total = nrows * upr;
-  const int64_t lb = blockIdx.x;  // plain order: spreads each XCD's writes over the output
+  const int64_t lb = blockIdx.x;
   const int64_t step = (int64_t)gridDim.x * blockDim.x * kIlp;
   for (int64_t base = lb * blockDim.x * kIlp + threadIdx.x; base < total; base += step) {
     int32_t s[kIlp];
@@ -234,20 +235,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
         v[i] = (int)(g - row[i] * upr);
       }
       s[i] = -1;
-      if (g < total) {
-        int64_t srow = row[i];
-        if (SEG) {  // record-major row (b,t,c,j) -> segment-major (b,c,t,j)
-          const int64_t r = row[i] / k;
-          const int64_t j = row[i] - r * k;
-          const int64_t TC = T * C;
-          const int64_t b = r / TC;
-          const int64_t tc = r - b * TC;
-          const int64_t t = tc / C;
-          const int64_t c = tc - t * C;
-          srow = (((b * C + c) * T) + t) * k + j;
-        }
-        s[i] = src[srow];
-      }
+      if (g < total) s[i] = src[row[i]];
     }
     V val[kIlp];
 #pragma unroll
@@ -263,23 +251,19 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
       const int64_t g = base + (int64_t)i * blockDim.x;
       if (g < total) {
         __builtin_nontemporal_store(val[i], &out[g]);
-        if (v[i] == 0) {
-          if (mask) mask[row[i]] = s[i] >= 0 ? 1 : 0;
-          if (SEG && src_out) src_out[row[i]] = s[i];
-        }
+        if (v[i] == 0 && mask) mask[row[i]] = s[i] >= 0 ? 1 : 0;
       }
     }
   }
 }
 
-template <typename V, bool SEG>
+template <typename V>
 hipError_t gather_typed(const void* rows, const int32_t* src, int64_t nrows, int upr, int64_t nsrc,
-                        int64_t T, int64_t C, int k, void* out, uint8_t* mask, int32_t* src_out,
-                        hipStream_t s) {
+                        void* out, uint8_t* mask, hipStream_t s) {
   const unsigned grid = xcd_grid(nrows * upr, 256 * kIlp);
   const V* r = (const V*)rows;
   V* o = (V*)out;
-#define REM_G(SH) gather_rows_kernel<V, SH, SEG><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, T, C, k, o, mask, src_out)
+#define REM_G(SH) gather_rows_kernel<V, SH><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask)
   switch (upr) {
     case 1: REM_G(0); break;
     case 2: REM_G(1); break;
@@ -293,36 +277,108 @@ hipError_t gather_typed(const void* rows, const int32_t* src, int64_t nrows, int
   return hipGetLastError();
 }
 
-template <bool SEG>
-hipError_t gather_dispatch(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
-                           int64_t row_bytes, int64_t T, int64_t C, int k, void* out,
-                           uint8_t* mask, int32_t* src_out, hipStream_t s) {
-  if (nrows == 0) return hipSuccess;
-  const uintptr_t align = (uintptr_t)rows | (uintptr_t)out | (uintptr_t)row_bytes;
-  if ((align & 15) == 0)
-    return gather_typed<u32x4, SEG>(rows, src, nrows, (int)(row_bytes / 16), nsrc, T, C, k, out, mask, src_out, s);
-  if ((align & 7) == 0)
-    return gather_typed<u32x2, SEG>(rows, src, nrows, (int)(row_bytes / 8), nsrc, T, C, k, out, mask, src_out, s);
-  if ((align & 3) == 0)
-    return gather_typed<uint32_t, SEG>(rows, src, nrows, (int)(row_bytes / 4), nsrc, T, C, k, out, mask, src_out, s);
-  if ((align & 1) == 0)
-    return gather_typed<uint16_t, SEG>(rows, src, nrows, (int)(row_bytes / 2), nsrc, T, C, k, out, mask, src_out, s);
-  return gather_typed<uint8_t, SEG>(rows, src, nrows, (int)row_bytes, nsrc, T, C, k, out, mask, src_out, s);
+
+// Segment-major [B][C][T][k] -> record-major [B][T][C][k], one tile of
+// tc heads x tt time steps per block through LDS: the reads are runs of tt*k
+// words of one segment, the writes runs of tc*k words of one time step (the
+// whole tile is one contiguous run when tc == C).  tc * tt * k <= kTileWords.
+constexpr int kTileWords = 4096;
+
+// Launched with exactly 256 threads.
+__global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __restrict__ src_seg,
+                                                              int64_t T, int64_t C, int k, int tc,
+                                                              int tt, int64_t ntt, int64_t ntc,
+                                                              int32_t* __restrict__ out) {
+  __shared__ int32_t lds[kTileWords + 64];
+  const int64_t tile = blockIdx.x;
+  const int64_t ct = tile % ntc;
+  const int64_t rest = tile / ntc;
+  const int64_t t0 = (rest % ntt) * tt;
+  const int64_t b = rest / ntt;
+  const int64_t c0 = ct * tc;
+  const int nt = (int)min<int64_t>(tt, T - t0);
+  const int nc = (int)min<int64_t>(tc, C - c0);
+  const int row = tt * k + 1;  // padded LDS row of one head
+  const int nq = nt * k;
+  const int n = nc * nq;
+  // All loads of a thread are issued before the first LDS store.
+  constexpr int kPer = kTileWords / 256;
+  int32_t v[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = threadIdx.x + r * 256;
+    if (i < n) {
+      const int cc = i / nq;
+      v[r] = src_seg[((b * C + c0 + cc) * T + t0) * k + (i - cc * nq)];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = threadIdx.x + r * 256;
+    if (i < n) {
+      const int cc = i / nq;
+      lds[cc * row + (i - cc * nq)] = v[r];
+    }
+  }
+  __syncthreads();
+  const int ck = nc * k;
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int i = threadIdx.x + r * 256;
+    if (i < n) {
+      const int ti = i / ck;
+      const int rem = i - ti * ck;
+      const int cc = rem / k;
+      const int j = rem - cc * k;
+      out[((b * T + t0 + ti) * C + c0) * k + rem] = lds[cc * row + ti * k + j];
+    }
+  }
 }
 
-__global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __restrict__ src_seg,
-                                                              int64_t rows, int64_t T, int64_t C,
-                                                              int k, int32_t* __restrict__ out) {
-  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < rows;
-       g += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = g / k;
-    const int64_t j = g - r * k;
-    const int64_t TC = T * C;
-    const int64_t b = r / TC;
-    const int64_t tc = r - b * TC;
-    const int64_t t = tc / C;
-    const int64_t c = tc - t * C;
-    out[g] = src_seg[(((b * C + c) * T) + t) * k + j];
+// The same for k == 1, C = 2^LOGC heads (2..16) and T % 4 == 0, with 16-byte
+// loads, LDS stores and global stores.  The tile is all C heads x TT time
+// steps, so the output of a block is one contiguous run of 4096 words.
+// Launched with exactly 256 threads.
+template <int LOGC>
+__global__ __launch_bounds__(256) void src_transpose_pow2_kernel(const int32_t* __restrict__ src_seg,
+                                                                int64_t T, int64_t ntt,
+                                                                int32_t* __restrict__ out) {
+  constexpr int C = 1 << LOGC;
+  constexpr int TT = kTileWords >> LOGC;
+  constexpr int ROW = TT + 4;  // padded head row, 16-byte aligned
+  constexpr int Q = TT / 4;    // 16-byte units per head row
+  constexpr int kPer = kTileWords / 4 / 256;
+  __shared__ __align__(16) int32_t lds[C * ROW];
+  const int64_t b = blockIdx.x / ntt;
+  const int64_t t0 = (blockIdx.x - b * ntt) * TT;
+  const int nt = (int)min<int64_t>(TT, T - t0);  // a multiple of 4
+  u32x4 v[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int idx = threadIdx.x + r * 256;
+    const int c = idx / Q, q = idx % Q;
+    if (4 * q < nt) v[r] = *(const u32x4*)(src_seg + (b * C + c) * T + t0 + 4 * q);
+  }
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int idx = threadIdx.x + r * 256;
+    const int c = idx / Q, q = idx % Q;
+    if (4 * q < nt) *(u32x4*)&lds[c * ROW + 4 * q] = v[r];
+  }
+  __syncthreads();
+  u32x4* o = (u32x4*)(out + (b * T + t0) * C);
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const int idx = threadIdx.x + r * 256;
+    const int f = 4 * idx;  // flat (t, c) position in the tile
+    if (f < nt * C) {
+      u32x4 w;
+      w.x = (uint32_t)lds[((f + 0) & (C - 1)) * ROW + ((f + 0) >> LOGC)];
+      w.y = (uint32_t)lds[((f + 1) & (C - 1)) * ROW + ((f + 1) >> LOGC)];
+      w.z = (uint32_t)lds[((f + 2) & (C - 1)) * ROW + ((f + 2) >> LOGC)];
+      w.w = (uint32_t)lds[((f + 3) & (C - 1)) * ROW + ((f + 3) >> LOGC)];
+      o[idx] = w;
+    }
   }
 }
 
@@ -354,17 +410,22 @@ hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s) {
   return hipGetLastError();
 }
 
+static bool link_lds_applies(const Tape& tp, int k) {
+  const int64_t nchunk = (tp.T + kLinkLdsWords - 1) / kLinkLdsWords;
+  return k == 1 && nchunk >= 1 && nchunk <= 8;  // segment read amplification <= 8x
+}
+
 template <typename U>
-hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s) {
+hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s) {
   const int64_t N = tp.n();
   const int64_t nchunk = (tp.T + kLinkLdsWords - 1) / kLinkLdsWords;
-  if (k == 1 && nchunk >= 1 && nchunk <= 8) {  // segment read amplification <= 8x
+  if (link_lds_applies(tp, k)) {
     const unsigned grid = xcd_grid(tp.nseg() * nchunk, 1, (int64_t)1 << 31);
     link1_lds_kernel<U><<<grid, kLinkThreads, 0, s>>>(sorted, tp.T, tp.C, tp.tbits, kLinkLdsWords,
-                                                      (int)nchunk, tp.nseg(), src_seg);
+                                                      (int)nchunk, tp.nseg(), src);
     return hipGetLastError();
   }
-  link_same_kernel<U><<<xcd_grid(N, 256), 256, 0, s>>>(sorted, N, tp.T, k, src_seg, tp.tbits, tp.C);
+  link_same_kernel<U><<<xcd_grid(N, 256), 256, 0, s>>>(sorted, N, tp.T, k, src, tp.tbits, tp.C);
   return hipGetLastError();
 }
 
@@ -386,21 +447,50 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
 
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
                             hipStream_t s) {
-  const int64_t rows = tp.n() * k;
-  src_record_major_kernel<<<grid_for(rows, 256), 256, 0, s>>>(src_seg, rows, tp.T, tp.C, k, out);
+  if (tp.n() == 0) return hipSuccess;
+  if (k > kTileWords) return hipErrorInvalidValue;
+  const bool vec = k == 1 && tp.C >= 2 && tp.C <= 16 && (tp.C & (tp.C - 1)) == 0 &&
+                   tp.T % 4 == 0 && (((uintptr_t)src_seg | (uintptr_t)out) & 15) == 0;
+  if (vec) {
+    const int logc = __builtin_ctzll((unsigned long long)tp.C);
+    const int64_t ntt = (tp.T + (kTileWords >> logc) - 1) / (kTileWords >> logc);
+    if (tp.B * ntt > INT32_MAX) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)(tp.B * ntt);
+    switch (logc) {
+      case 1: src_transpose_pow2_kernel<1><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
+      case 2: src_transpose_pow2_kernel<2><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
+      case 3: src_transpose_pow2_kernel<3><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
+      default: src_transpose_pow2_kernel<4><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
+    }
+    return hipGetLastError();
+  }
+  // Heads per tile: all of them up to 16 (a contiguous output run), time
+  // steps to fill the tile.
+  const int tc = (int)std::min<int64_t>({tp.C, 16, kTileWords / k});
+  const int tt = (int)std::min<int64_t>(tp.T, kTileWords / (tc * k));
+  const int64_t ntt = (tp.T + tt - 1) / tt;
+  const int64_t ntc = (tp.C + tc - 1) / tc;
+  const int64_t blocks = tp.B * ntt * ntc;
+  if (blocks > INT32_MAX) return hipErrorInvalidValue;
+  src_record_major_kernel<<<(unsigned)blocks, 256, 0, s>>>(src_seg, tp.T, tp.C, k, tc, tt, ntt, ntc,
+                                                           out);
   return hipGetLastError();
 }
 
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s) {
-  return gather_dispatch<false>(rows, nsrc, src, nrows, row_bytes, 1, 1, 1, out, mask, nullptr, s);
-}
-
-hipError_t gather_rows_segmajor(const void* rows, const int32_t* src_seg, const Tape& tp, int k,
-                                int64_t row_bytes, void* out, uint8_t* mask, int32_t* src_out,
-                                hipStream_t s) {
-  return gather_dispatch<true>(rows, tp.n(), src_seg, tp.n() * k, row_bytes, tp.T, tp.C, k, out,
-                               mask, src_out, s);
+  if (nrows == 0) return hipSuccess;
+  // The widest unit that the row size and both base addresses allow.
+  const uintptr_t align = (uintptr_t)rows | (uintptr_t)out | (uintptr_t)row_bytes;
+  if ((align & 15) == 0)
+    return gather_typed<u32x4>(rows, src, nrows, (int)(row_bytes / 16), nsrc, out, mask, s);
+  if ((align & 7) == 0)
+    return gather_typed<u32x2>(rows, src, nrows, (int)(row_bytes / 8), nsrc, out, mask, s);
+  if ((align & 3) == 0)
+    return gather_typed<uint32_t>(rows, src, nrows, (int)(row_bytes / 4), nsrc, out, mask, s);
+  if ((align & 1) == 0)
+    return gather_typed<uint16_t>(rows, src, nrows, (int)(row_bytes / 2), nsrc, out, mask, s);
+  return gather_typed<uint8_t>(rows, src, nrows, (int)row_bytes, nsrc, out, mask, s);
 }
 
 template hipError_t link_same<uint32_t>(const uint32_t*, const Tape&, int, int32_t*, hipStream_t);
