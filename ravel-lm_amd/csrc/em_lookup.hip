@@ -108,6 +108,14 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
   const U* sk = sorted + (live ? seg : 0) * T;
   const int64_t nround = nslot > 0 ? (T + ROUND - 1) / ROUND : 0;
   const bool aligned = (T % VEC) == 0;  // vector loads need T*sizeof(U) 16-byte aligned rows
+  // Every key of the segment is tested against this chunk, so the per-key test
+  // is kept to 32-bit arithmetic: t - t_lo < nslot (unsigned) and equal
+  // address bits ((pk ^ u) < 2^tbits).  The source (b*T + t')*C + c < N < 2^31.
+  const uint32_t tlo = (uint32_t)t_lo;
+  const uint32_t nsl = (uint32_t)nslot;
+  const U same_bound = (U)1 << tbits;  // tbits < bit width of U
+  const int32_t vbase = (int32_t)((b * T) * C + c);
+  const int32_t Ci = (int32_t)C;
   for (int64_t r0 = 0; r0 < nround; ++r0) {
     const int64_t base = r0 * ROUND;
     const int xb = (int)(r0 & 1);
@@ -135,17 +143,27 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
       if (lane == 0) {
         if (w > 0) prev = xch[xb][r][w - 1];
         else if (r > 0) prev = xch[xb][r - 1][kLinkWaves - 1];
-        else prev = xch[xb ^ 1][kLinkRows - 1][kLinkWaves - 1];  // previous round (unused at p = 0)
+        else if (r0 > 0) prev = xch[xb ^ 1][kLinkRows - 1][kLinkWaves - 1];
+        else prev = ~v[0][0];  // position 0 has no predecessor: differs in the address bits
       }
+      if (p0 + VEC <= T) {  // the common case: every key of the vector is real
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int64_t p = p0 + e;
-        const U u = v[r][e];
-        const U pk = e > 0 ? v[r][e - 1] : prev;
-        const int64_t t = (int64_t)(u & tmask);
-        if (p < T && p > 0 && t >= t_lo && t < t_hi && (pk >> tbits) == (u >> tbits) &&
-            (int64_t)(pk & tmask) < T)
-          buf[t - t_lo] = (int32_t)((b * T + (int64_t)(pk & tmask)) * C + c);
+        for (int e = 0; e < VEC; ++e) {
+          const U u = v[r][e];
+          const U pk = e > 0 ? v[r][e - 1] : prev;
+          const uint32_t off = (uint32_t)(u & tmask) - tlo;
+          if (off < nsl && (U)(pk ^ u) < same_bound)
+            buf[off] = vbase + (int32_t)(pk & tmask) * Ci;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const U u = v[r][e];
+          const U pk = e > 0 ? v[r][e - 1] : prev;
+          const uint32_t off = (uint32_t)(u & tmask) - tlo;
+          if (p0 + e < T && off < nsl && (U)(pk ^ u) < same_bound)
+            buf[off] = vbase + (int32_t)(pk & tmask) * Ci;
+        }
       }
     }
     __syncthreads();  // xch[xb ^ 1] is rewritten next round
