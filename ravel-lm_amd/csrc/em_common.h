@@ -54,6 +54,29 @@ constexpr int kXcds = 8;
 __device__ __forceinline__ uint32_t xcd_block(uint32_t bid, uint32_t nblk) {
   return (bid % kXcds) * (nblk / kXcds) + bid / kXcds;
 }
+// Division of n in [0, 2^31) by a divisor fixed at launch, by multiply-high
+// and shift (the round-up method of Granlund and Montgomery, "Division by
+// invariant integers using multiplication", 1994): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(m, n) + n) >> l.
+struct FastDiv {
+  uint32_t d, m, l;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  f.l = 0;
+  while (((uint64_t)1 << f.l) < d) ++f.l;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << f.l) - d)) / d + 1);
+  return f;
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(f.m, n) + n) >> f.l;
+}
+// n / d where d is uniform over the block and usually f.d.
+__device__ __forceinline__ uint32_t fdiv_or(uint32_t n, const FastDiv& f, uint32_t d) {
+  return d == f.d ? fdiv(n, f) : n / d;
+}
+
 // Groups of G consecutive logical blocks on one XCD, successive groups on
 // successive XCDs (the grid must be a multiple of kXcds * G).
 __device__ __forceinline__ uint32_t xcd_group_block(uint32_t bid, uint32_t G) {
@@ -72,15 +95,26 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 
 // Lanes of the wave whose 8-bit digit equals this lane's digit.
+// One ballot per bit; a lane is a mismatch if it differs in any bit.  With
+// s = 0 or ~0 (this lane's bit, sign-extended), the lanes that differ in the
+// bit are ballot ^ s, so each bit costs a bit-extract, a compare and one
+// xor-or per 32-lane half.
 __device__ __forceinline__ uint64_t match_byte(uint32_t d) {
-  uint64_t peers = ~0ull;
+  uint32_t miss_lo = 0, miss_hi = 0;
 #pragma unroll
   for (int bit = 0; bit < 8; ++bit) {
-    const bool on = (d >> bit) & 1u;
-    const uint64_t m = __ballot(on);
-    peers &= on ? m : ~m;
+    const uint32_t s = (uint32_t)((int32_t)(d << (31 - bit)) >> 31);
+    const uint64_t m = __ballot(s != 0);
+    miss_lo |= (uint32_t)m ^ s;
+    miss_hi |= (uint32_t)(m >> 32) ^ s;
   }
-  return peers;
+  return ~(((uint64_t)miss_hi << 32) | miss_lo);
+}
+
+// Number of lanes below this one in mask (v_mbcnt).
+__device__ __forceinline__ uint32_t count_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
 __device__ __forceinline__ int64_t reduce_addr(int64_t a, int64_t A, int mode, bool trunc32) {

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kSortThreads) void hist_kernel(const U* __restrict_
     const bool valid = idx < n;
     const uint32_t d = (uint32_t)(key[i] >> shift) & (kRadix - 1);
     const uint64_t peers = match_byte(d) & __ballot(valid);
-    if (valid && (int)__lane_id() == __ffsll((unsigned long long)peers) - 1)
+    if (valid && count_below(peers) == 0)  // the lowest lane of the digit adds for all
       atomicAdd(&h[d], (uint32_t)__popcll(peers));
   }
   __syncthreads();
@@ -146,11 +146,12 @@ __global__ __launch_bounds__(kSortThreads) void scatter_kernel(const U* __restri
     const uint64_t peers = match_byte(d) & __ballot(valid);
     uint32_t old = 0;
     if (valid) old = wcnt[w][d];
+    const uint32_t below = count_below(peers);
     __builtin_amdgcn_wave_barrier();
-    if (valid && lane == __ffsll((unsigned long long)peers) - 1)
+    if (valid && below == 0)  // the lowest lane of the digit advances the counter
       wcnt[w][d] = old + (uint32_t)__popcll(peers);
     __builtin_amdgcn_wave_barrier();
-    rank[i] = old + (uint32_t)__popcll(peers & lanemask_lt());
+    rank[i] = old + below;
   }
   __syncthreads();
 
@@ -264,7 +265,8 @@ template <typename U, typename AT>
 __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const AT* __restrict__ addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int npass, int ntiles,
-    int64_t nlogical, U* __restrict__ keys, uint32_t* __restrict__ hist) {
+    int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
+    uint32_t* __restrict__ hist) {
   __shared__ U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
@@ -289,14 +291,14 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
 #pragma unroll
     for (int j = 0; j < kPackBatch; ++j) {  // all loads first: one memory latency per batch
       const int i = i0 + j * kPackThreads + threadIdx.x;
-      const int tl = i / cc;
+      const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)cc);
       av[j] = i < n ? arow[(int64_t)tl * C + (i - tl * cc)] : AT(0);
     }
 #pragma unroll
     for (int j = 0; j < kPackBatch; ++j) {
       const int i = i0 + j * kPackThreads + threadIdx.x;
       if (i < n) {
-        const int tl = i / cc;
+        const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)cc);
         const int cl = i - tl * cc;
         int64_t a = reduce_addr((int64_t)av[j], A, mode, trunc32 != 0);
         if (wmask && !wmask[b * T + t0 + tl]) a = A;
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
   }
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += kPackThreads) {
-    const int cl = i / tt;
+    const int cl = (int)fdiv_or((uint32_t)i, by_tt, (uint32_t)tt);
     const int tl = i - cl * tt;
     keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
   }
@@ -418,11 +420,12 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
     const uint64_t peers = match_byte(d) & __ballot(valid);
     uint32_t old = 0;
     if (valid) old = wcnt[w][d];
+    const uint32_t below = count_below(peers);
     __builtin_amdgcn_wave_barrier();
-    if (valid && lane == __ffsll((unsigned long long)peers) - 1)
+    if (valid && below == 0)  // the lowest lane of the digit advances the counter
       wcnt[w][d] = old + (uint32_t)__popcll(peers);
     __builtin_amdgcn_wave_barrier();
-    rank[i] = old + (uint32_t)__popcll(peers & lanemask_lt());
+    rank[i] = old + below;
   }
   __syncthreads();
   uint32_t tot = 0;
@@ -702,14 +705,17 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   uint32_t* err = tickets + (int64_t)npass * tp.nseg();
   const int64_t nlogical = tp.B * nt0 * ncg;
   const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
+  // Divisors of the pack index math (the last head group / time tile of a row
+  // may be smaller and then divides the slow way).
+  const FastDiv by_cc = make_fastdiv((uint32_t)pl.CC), by_tt = make_fastdiv((uint32_t)tt);
   if (addr64)
     pack_hist_kernel<U, int64_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int64_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, ka, hist);
+        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist);
   else
     pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, ka, hist);
+        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist);
   // Few pack tiles per segment: scatter and sweep blocks sum the histograms
   // themselves; otherwise one scan kernel prepares offsets and digit bases.
   const bool direct = nt0 <= kDirectMaxTiles;
