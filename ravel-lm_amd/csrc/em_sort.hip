@@ -239,8 +239,8 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
 }
 
 // ------------------------------------------------------------------------
-// Fused path.  pack_hist -> scan_hist -> scatter (pass 0, reduce-then-scan)
-// -> sweep (passes >= 1, decoupled look-back).  Used when the per-block LDS
+// Fused path.  pack_hist -> seg_offsets or scan_hist -> scatter0 (pass 0,
+// reduce-then-scan) -> sweep (passes >= 1, decoupled look-back).  Used when the per-block LDS
 // budget below holds; the generic path above handles every other shape.
 
 constexpr int kPackThreads = 512;
@@ -441,10 +441,11 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
 
 // Stage the ranked tile in LDS in local sorted order, then write each digit's
 // run to its global position (gbase[d] + local index), bounded by the segment.
+// Positions are segment-relative and T < 2^30 on this path, so int32 holds them.
 template <typename U, int ITEMS>
 __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* rank, int n,
                                                 int shift, uint32_t (*wcnt)[kRadix],
-                                                const uint32_t* dstart, const int64_t* gbase,
+                                                const uint32_t* dstart, const int32_t* gbase,
                                                 U* stage, U* __restrict__ dst, int64_t T) {
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
 #pragma unroll
@@ -456,37 +457,58 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < n; idx += kSortThreads) {
-    const U k = stage[idx];
-    const uint32_t d = (uint32_t)(k >> shift) & (kRadix - 1);
-    const int64_t pos = gbase[d] + idx;
-    if (pos >= 0 && pos < T) dst[pos] = k;
+  // All LDS reads first, then the stores: one LDS round trip, not one per key.
+  U k[ITEMS];
+  int32_t pos[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = i * kSortThreads + tid;
+    k[i] = idx < n ? stage[idx] : U(0);
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    pos[i] = gbase[(uint32_t)(k[i] >> shift) & (kRadix - 1)] + i * kSortThreads + tid;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = i * kSortThreads + tid;
+    if (idx < n && (uint32_t)pos[i] < (uint32_t)T) dst[pos[i]] = k[i];
   }
 }
 
-// Tile prefix and digit base of one pass, read straight from the pack
-// histograms of the segment (used when a segment has few pack tiles): thread
-// d returns sum_{j < upto} hist[j][pass][d] + (exclusive scan over digits of
-// sum_j hist[j][pass][d]).  All threads must call it (it synchronizes).
-constexpr int kDirectMaxTiles = 64;
+// Pass offsets of a segment with at most kShortMaxTiles pack tiles: one block
+// per (segment, pass), thread d = digit.  binbase[seg][pass][d] = exclusive
+// scan over digits of the segment's digit totals; for pass 0 also
+// offs[seg][scatter tile][d] = count of digit d in the earlier scatter tiles
+// (2^lm pack tiles each).  Resets the look-back tickets and the error word.
+constexpr int kShortMaxTiles = 64;
 
-__device__ __forceinline__ int64_t direct_offset(const uint32_t* __restrict__ hs, int nt0, int per,
-                                                 int pass, int upto, uint32_t* scan_tmp) {
+__global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
+    const uint32_t* __restrict__ hist, int nt0, int lm, int npass, uint32_t* __restrict__ offs,
+    int nsct, uint32_t* __restrict__ binbase, uint32_t* __restrict__ tickets, int64_t nseg) {
+  __shared__ uint32_t tmp[kSortThreads / kWave + 1];
   const int d = threadIdx.x;
-  uint32_t pre = 0, tot = 0;
-  for (int j0 = 0; j0 < nt0; j0 += 16) {
-    uint32_t v[16];
+  const int64_t seg = blockIdx.x / npass;
+  const int p = (int)(blockIdx.x - seg * npass);
+  const int per = npass * kRadix;
+  const uint32_t* hs = hist + seg * (int64_t)nt0 * per + p * kRadix + d;
+  uint32_t v[kShortMaxTiles];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      v[j] = (j0 + j < nt0) ? hs[(int64_t)(j0 + j) * per + pass * kRadix + d] : 0u;
+  for (int j = 0; j < kShortMaxTiles; ++j) v[j] = j < nt0 ? hs[(int64_t)j * per] : 0u;
+  uint32_t tot = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      tot += v[j];
-      if (j0 + j < upto) pre += v[j];
+  for (int j = 0; j < kShortMaxTiles; ++j) tot += v[j];
+  binbase[(seg * npass + p) * kRadix + d] = block_excl_scan<kSortThreads>(tot, tmp, nullptr);
+  if (p == 0) {
+    const int mmask = (1 << lm) - 1;
+    uint32_t run = 0;
+#pragma unroll
+    for (int j = 0; j < kShortMaxTiles; ++j) {
+      if (j < nt0 && (j & mmask) == 0) offs[(seg * nsct + (j >> lm)) * kRadix + d] = run;
+      run += v[j];
     }
   }
-  const uint32_t base = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
-  return (int64_t)pre + (int64_t)base;
+  if (d == 0) tickets[(int64_t)p * nseg + seg] = 0;  // [pass][seg]
+  if (blockIdx.x == 0 && d == 0) tickets[(int64_t)npass * nseg] = 0;  // error word
 }
 
 __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t words) {
@@ -499,19 +521,17 @@ __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t wor
 
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
-    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ hist, int nt0,
-    int m, const uint32_t* __restrict__ offs, const uint32_t* __restrict__ binbase, int npass,
-    int64_t T, int ntiles, int64_t nblk, int shift, uint32_t* __restrict__ zero0, int64_t zero0_words,
-    uint32_t* __restrict__ zero1, int64_t zero1_words) {
+    const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
+    const uint32_t* __restrict__ binbase, int npass, int64_t T, int ntiles, int64_t nblk,
+    int shift, uint32_t* __restrict__ zero0, int64_t zero0_words) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
   __shared__ uint32_t dstart[kRadix];
-  __shared__ int64_t gbase[kRadix];
+  __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ U stage[TILE];
   zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
-  zero_slice(zero1, zero1_words);
   const int tid = threadIdx.x;
   // Consecutive tiles of a segment on one XCD: their partial output lines merge in one L2.
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
@@ -520,20 +540,14 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   const int tile = (int)(lb - seg * ntiles);
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  const int per = npass * kRadix;
-  int64_t gofs;
-  if (offs) {  // offsets from the scan kernel
-    gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
-           (int64_t)binbase[seg * npass * kRadix + tid];
-  } else {
-    gofs = direct_offset(hist + seg * (int64_t)nt0 * per, nt0, per, 0, tile * m, scan_tmp);
-  }
   U key[ITEMS];
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
+  const int64_t gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
+                       (int64_t)binbase[seg * npass * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
   rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
-  gbase[tid] = gofs - (int64_t)dstart[tid];
+  gbase[tid] = (int32_t)(gofs - (int64_t)dstart[tid]);
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
 }
@@ -541,15 +555,14 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ binbase_p,
-    const uint32_t* __restrict__ hist, int nt0, int pass, int npass,
-    uint32_t* __restrict__ status, uint32_t* __restrict__ ticket, int64_t T, int ntiles,
+    int npass, uint32_t* __restrict__ status, uint32_t* __restrict__ ticket, int64_t T, int ntiles,
     int64_t nblk, int shift, uint32_t* __restrict__ next_status, int64_t next_words,
     uint32_t* __restrict__ err) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
   __shared__ uint32_t dstart[kRadix];
-  __shared__ int64_t gbase[kRadix];
+  __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ uint32_t s_ticket;
   __shared__ U stage[TILE];
@@ -567,12 +580,9 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   if (tile >= ntiles) return;  // uniform per block; tickets run 0..ntiles-1
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  const int64_t base_d =
-      binbase_p ? (int64_t)binbase_p[seg * npass * kRadix + tid]
-                : direct_offset(hist + seg * (int64_t)nt0 * npass * kRadix, nt0, npass * kRadix,
-                                pass, 0, scan_tmp);
   U key[ITEMS];
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
+  const int64_t base_d = (int64_t)binbase_p[seg * npass * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
   rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
@@ -617,7 +627,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   if (tile > 0)
     __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kFlagP | ((excl + own) & kValMask),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  gbase[tid] = base_d + (int64_t)excl - (int64_t)dstart[tid];
+  gbase[tid] = (int32_t)(base_d + (int64_t)excl - (int64_t)dstart[tid]);
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
 }
@@ -716,19 +726,22 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
     pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
         pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist);
-  // Few pack tiles per segment: scatter and sweep blocks sum the histograms
-  // themselves; otherwise one scan kernel prepares offsets and digit bases.
-  const bool direct = nt0 <= kDirectMaxTiles;
-  const int64_t ticket_words = (int64_t)(npass + 1) * tp.nseg();  // [pass][seg] + error word
-  if (!direct)
+  // Pass-0 tile offsets and the digit bases of every pass, from the pack
+  // histograms: one block per (segment, pass) for short segments, else one
+  // 1024-thread block per segment.
+  if (nt0 <= kShortMaxTiles) {
+    const int lm = __builtin_ctz((unsigned)m);
+    seg_offsets_kernel<<<(unsigned)(tp.nseg() * npass), kSortThreads, 0, s>>>(
+        hist, nt0, lm, npass, offs, nsct, binbase, tickets, tp.nseg());
+  } else {
     scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, npass, offs, nsct, binbase,
                                                            tickets);
+  }
   const int64_t nblk0 = tp.nseg() * nsct;
   const unsigned g0 = xcd_grid(nblk0, 1, (int64_t)1 << 31);
   uint32_t* next0 = npass > 1 ? status[0] : nullptr;
   scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
-      ka, kb, hist, nt0, m, direct ? nullptr : offs, binbase, npass, tp.T, nsct, nblk0, tp.tbits,
-      next0, status_words, direct ? tickets : nullptr, ticket_words);
+      ka, kb, offs, binbase, npass, tp.T, nsct, nblk0, tp.tbits, next0, status_words);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   U* cur = kb;
@@ -738,7 +751,7 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   for (int p = 1; p < npass; ++p) {
     uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
     sweep_kernel<U, kSweepItems><<<gs, kSortThreads, 0, s>>>(
-        cur, alt, direct ? nullptr : binbase + p * kRadix, hist, nt0, p, npass,
+        cur, alt, binbase + p * kRadix, npass,
         status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts, nblks, tp.tbits + 8 * p, next,
         status_words, err);
     e = hipGetLastError();

@@ -116,6 +116,8 @@ SMALL = [
     (1, 3000, 40, 1 << 20, None, None, False, False, 2),  # 3 passes x 40 heads: generic sort
     (1, 300, 200, 50, None, None, False, True, 1),  # 200 heads: pack tile over the LDS budget
     (2, 9000, 3, 1 << 17, None, None, True, False, 2),  # masked, 3 passes, 2 look-back sweeps
+    (1, 65536, 2, 3, None, None, False, False, 1),  # one-chunk link at its longest segment
+    (1, 70000, 2, 50, None, None, False, False, 1),  # link in 16384-step chunks (T > 65536)
 ]
 
 
