@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--adversarial", action="store_true", help="90%% of records at address 0")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--suite", action="store_true",
+                    help="time every BASELINE config (cfg1-cfg5), one JSON line per op, instead of the headline")
     return ap.parse_args()
 
 
@@ -101,6 +103,11 @@ def main():
     from ravel_em import causal_last_k_lookup, workloads
 
     dev = torch.device("cuda", 0)
+    if args.suite:
+        from ravel_em import suite
+
+        suite.run(dev)
+        return
     log("generating cfg4 inputs on the device")
     w = workloads.cfg4(dev, adversarial=args.adversarial)
     B, T, C, D = w.shape
