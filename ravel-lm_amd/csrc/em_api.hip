@@ -209,6 +209,8 @@ struct SumWs {
   void* S;
   int32_t* spos;
   void* gacc;
+  uint64_t* walk;
+  int64_t walk_words;
 };
 
 template <typename U>
@@ -220,6 +222,8 @@ SumWs<U> take_sum(Bump& bp, const Tape& tp, int64_t D, int dtype, bool direct, b
   w.tail = bp.take<char>(nch * (size_t)D * ab);
   w.flag = bp.take<uint8_t>(nch);
   w.carry = bp.take<char>(nch * (size_t)D * ab);
+  w.walk_words = (int64_t)seg_sum_walk_words(tp, D, dtype);
+  w.walk = bp.take<uint64_t>((size_t)w.walk_words);
   if (!direct) {
     w.spos = bp.take<int32_t>((size_t)tp.n());
     if (backward)
@@ -240,18 +244,20 @@ int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s);
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s,
+                              (uint32_t*)w.walk, 2 * w.walk_words);
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (direct) {
     stage_begin(kStageSum, s);
     e = seg_sum<U>(sorted, payload, dtype, tp, D, true, out_sum, out_mask, w.tail, w.flag,
-                   w.carry, s);
+                   w.carry, w.walk, s);
     stage_end(kStageSum, s);
     if (e != hipSuccess) return hip_fail(e, "segmented sum");
     return RAVEL_EM_OK;
   }
-  e = seg_sum<U>(sorted, payload, dtype, tp, D, false, w.S, nullptr, w.tail, w.flag, w.carry, s);
+  e = seg_sum<U>(sorted, payload, dtype, tp, D, false, w.S, nullptr, w.tail, w.flag, w.carry,
+                 w.walk, s);
   if (e != hipSuccess) return hip_fail(e, "segmented sum");
   e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
@@ -269,14 +275,15 @@ int seg_sum_bwd_run(const void* waddr, const void* raddr, bool a64, const uint8_
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, true);
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s);
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s,
+                              (uint32_t*)w.walk, 2 * w.walk_words);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (!direct) {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
     if (e != hipSuccess) return hip_fail(e, "resolve");
   }
   e = seg_sum_bwd<U>(sorted, w.spos, grad, dtype, tp, D, direct, (float*)w.gacc, w.tail, w.flag,
-                     w.carry, grad_payload, s);
+                     w.carry, w.walk, grad_payload, s);
   if (e != hipSuccess) return hip_fail(e, "segmented sum backward");
   return RAVEL_EM_OK;
 }

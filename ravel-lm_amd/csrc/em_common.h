@@ -164,10 +164,12 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, u
 // All launchers enqueue on `s` and return hipGetLastError() of the last launch.
 
 // Sort every segment of the tape by packed key.  Returns the buffer (ka or kb)
-// holding the sorted keys in *sorted.
+// holding the sorted keys in *sorted.  The zero_words words at `zero` are set
+// to zero on the way (state that a later kernel of the same call needs clear).
 template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp,
-                     U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s);
+                     U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s,
+                     uint32_t* zero = nullptr, int64_t zero_words = 0);
 size_t sort_counts_words(const Tape& tp);
 size_t sort_fused_words(const Tape& tp, size_t key_bytes);
 
@@ -197,13 +199,17 @@ enum Stage : int { kStageSort = 0, kStageResolve, kStageGather, kStageSum, kStag
 void stage_begin(int stage, hipStream_t s);
 void stage_end(int stage, hipStream_t s);
 
-// Segmented causal sum over sorted runs.
+// Segmented causal sum over sorted runs.  `walk` (seg_sum_walk_words words,
+// zero on entry) is the state of the walker kernel, used when the row is a
+// whole number (1..64, a power of two) of 16-byte units; the chunk kernels
+// (tail/flag/carry) take every other shape.
 template <typename U>
 hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& tp, int64_t D,
                    bool direct, void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag,
-                   void* carry, hipStream_t s);
+                   void* carry, uint64_t* walk, hipStream_t s);
 size_t seg_sum_chunks(const Tape& tp);
 size_t acc_bytes(int dtype);
+size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype);
 
 // Backward of latest-k: grad_payload[src[r,j]] += grad_values[r,j].
 hipError_t latest_k_bwd_chain(const int32_t* src, const void* grad_values, int dtype, int64_t N,
@@ -214,7 +220,8 @@ hipError_t latest_k_bwd_atomic(const int32_t* src, const void* grad_values, int 
 template <typename U>
 hipError_t seg_sum_bwd(const U* sorted, const int32_t* spos, const void* grad_out, int dtype,
                        const Tape& tp, int64_t D, bool direct, float* gacc, void* tail,
-                       uint8_t* flag, void* carry, void* grad_payload, hipStream_t s);
+                       uint8_t* flag, void* carry, uint64_t* walk, void* grad_payload,
+                       hipStream_t s);
 
 // Decode cache (values [B*C, A, k, row], filled [B*C, A, k]).
 hipError_t cache_read(const void* values, const uint8_t* filled, const void* addr, bool addr64,

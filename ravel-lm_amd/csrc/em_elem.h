@@ -1,9 +1,9 @@
 // Payload element types and their accumulators.
 //
 // Sums accumulate 16-bit payloads in fp32 and 32/64-bit payloads in fp64, then
-// round once (round-to-nearest-even) to the payload dtype.  bf16 conversion is
-// the standard bias-and-truncate RNE on the fp32 bit pattern; fp16 uses the
-// hardware conversion (v_cvt_f16_f32, RNE).
+// round once (round-to-nearest-even) to the payload dtype.  Both 16-bit
+// conversions are the hardware ones of gfx950, two values per instruction
+// (v_cvt_pk_bf16_f32, v_cvt_pk_f16_f32; round to nearest even).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,11 +17,18 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 (a in the low half).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);  // quiet NaN
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
+  return (uint16_t)f32x2_to_bf16x2_bits(f, 0.0f);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
@@ -30,6 +37,11 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ uint32_t f32x2_to_f16x2_bits(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
 }
 
 template <int DT>
@@ -57,6 +69,7 @@ struct Elem<kBF16> {
   using acc_t = float;
   static __device__ __forceinline__ acc_t load(store_t x) { return bf16_bits_to_f32(x); }
   static __device__ __forceinline__ store_t store(acc_t v) { return f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ uint32_t store2(acc_t a, acc_t b) { return f32x2_to_bf16x2_bits(a, b); }
 };
 
 template <>
@@ -65,6 +78,7 @@ struct Elem<kF16> {
   using acc_t = float;
   static __device__ __forceinline__ acc_t load(store_t x) { return f16_bits_to_f32(x); }
   static __device__ __forceinline__ store_t store(acc_t v) { return f32_to_f16_bits(v); }
+  static __device__ __forceinline__ uint32_t store2(acc_t a, acc_t b) { return f32x2_to_f16x2_bits(a, b); }
 };
 
 }  // namespace rem

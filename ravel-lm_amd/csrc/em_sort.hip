@@ -256,6 +256,15 @@ constexpr int kPackBatch = 16;            // address loads in flight per pack th
 constexpr int kLookBatch = 16;            // predecessor tiles read per look-back round
 constexpr int kScatter0Items = 8;         // pass-0 scatter tile = 2048 keys
 
+// Block blockIdx.x's share of a zeroing of `words` words (all threads call it).
+__device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t words) {
+  if (!p) return;
+  const int64_t per = (words + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = (int64_t)blockIdx.x * per;
+  const int64_t hi = (lo + per) < words ? (lo + per) : words;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) p[i] = 0;
+}
+
 // One block packs TT time steps of CC heads of one batch row: the [TT, CC]
 // slab of the [B,T,C] address tensor goes through LDS into segment-major keys,
 // with per-(segment, tile) histograms of every digit pass.  Sibling head
@@ -266,9 +275,10 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const AT* __restrict__ addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int npass, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
-    uint32_t* __restrict__ hist) {
+    uint32_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
   __shared__ U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
+  zero_slice(zero, zero_words);  // every block, padding included
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
   if (logical >= nlogical) return;  // padding block of the XCD-rounded grid (uniform)
   const int cg = (int)(logical % ncg);
@@ -511,14 +521,6 @@ __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
   if (blockIdx.x == 0 && d == 0) tickets[(int64_t)npass * nseg] = 0;  // error word
 }
 
-__device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t words) {
-  if (!p) return;
-  const int64_t per = (words + gridDim.x - 1) / gridDim.x;
-  const int64_t lo = (int64_t)blockIdx.x * per;
-  const int64_t hi = (lo + per) < words ? (lo + per) : words;
-  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) p[i] = 0;
-}
-
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
@@ -695,7 +697,7 @@ size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
 template <typename U>
 static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* wmask,
                                   const Tape& tp, PackPlan pl, U* ka, U* kb, uint32_t* words,
-                                  U** sorted, hipStream_t s) {
+                                  U** sorted, hipStream_t s, uint32_t* zero, int64_t zero_words) {
   const int tt = pl.TT;
   const int ncg = (int)((tp.C + pl.CC - 1) / pl.CC);
   const int npass = (tp.abits + 7) / 8;
@@ -721,11 +723,11 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   if (addr64)
     pack_hist_kernel<U, int64_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int64_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist);
+        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
   else
     pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
         (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist);
+        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
   // Pass-0 tile offsets and the digit bases of every pass, from the pack
   // histograms: one block per (segment, pass) for short segments, else one
   // 1024-thread block per segment.
@@ -766,10 +768,17 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
 
 template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp, U* ka,
-                     U* kb, uint32_t* counts, U** sorted, hipStream_t s) {
+                     U* kb, uint32_t* counts, U** sorted, hipStream_t s, uint32_t* zero,
+                     int64_t zero_words) {
   if (tp.fused) {
     const PackPlan pl = fused_plan(tp, sizeof(U));
-    if (pl.TT) return sort_tape_fused<U>(addr, addr64, wmask, tp, pl, ka, kb, counts, sorted, s);
+    if (pl.TT)
+      return sort_tape_fused<U>(addr, addr64, wmask, tp, pl, ka, kb, counts, sorted, s, zero,
+                                zero_words);
+  }
+  if (zero && zero_words > 0) {
+    const hipError_t ez = fill_bytes(zero, 0, (size_t)zero_words * 4, s);
+    if (ez != hipSuccess) return ez;
   }
   const int tt = pack_tt(tp.C, sizeof(U));
   const size_t shm = (size_t)tp.C * (tt + 1) * sizeof(U);
@@ -825,9 +834,11 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 }
 
 template hipError_t sort_tape<uint32_t>(const void*, bool, const uint8_t*, const Tape&, uint32_t*,
-                                        uint32_t*, uint32_t*, uint32_t**, hipStream_t);
+                                        uint32_t*, uint32_t*, uint32_t**, hipStream_t, uint32_t*,
+                                        int64_t);
 template hipError_t sort_tape<uint64_t>(const void*, bool, const uint8_t*, const Tape&, uint64_t*,
-                                        uint64_t*, uint32_t*, uint64_t**, hipStream_t);
+                                        uint64_t*, uint32_t*, uint64_t**, hipStream_t, uint32_t*,
+                                        int64_t);
 template hipError_t emit_order<uint32_t>(const uint32_t*, const uint8_t*, int64_t*, const Tape&,
                                          void*, bool, int64_t*, hipStream_t);
 template hipError_t emit_order<uint64_t>(const uint64_t*, const uint8_t*, int64_t*, const Tape&,

@@ -31,6 +31,7 @@ namespace rem {
 namespace {
 
 constexpr int kChunk = 64;
+constexpr int kPartPos = 1024;  // walk positions per block of the walker kernel
 
 __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
@@ -107,13 +108,16 @@ __global__ __launch_bounds__(256) void segsum_local_kernel(
   const int64_t col = (int64_t)blockIdx.y * kWave + lane;
   const bool colok = col < D;
   const int64_t segbase = cv.seg * T;
+  // Every load is unconditional (a clamped row and column stand in for the
+  // positions and columns that do not exist), so all kChunk loads are in
+  // flight together; the walk below ignores the stand-ins.
+  const int64_t lcol = colok ? col : 0;
   XIn v[kChunk];
 #pragma unroll
   for (int i = 0; i < kChunk; ++i) {
-    if (i < cv.n) {
-      const int64_t row = IN_SORTED ? (segbase + readlane64(cv.pos, i)) : readlane64(cv.rec, i);
-      v[i] = colok ? in[row * D + col] : XIn(0);
-    }
+    const int ii = i < cv.n ? i : 0;
+    const int64_t row = IN_SORTED ? (segbase + readlane64(cv.pos, ii)) : readlane64(cv.rec, ii);
+    v[i] = in[row * D + lcol];
   }
   Acc acc = 0;
   bool seen = false;
@@ -214,10 +218,282 @@ __global__ __launch_bounds__(256) void segsum_fixup_kernel(
   }
 }
 
+// Flagged 64-bit words of the part aggregates: one per 32 bits of accumulator.
+size_t seg_sum_status_words(const Tape& tp, int64_t D, size_t acc_size) {
+  const int64_t nparts = (tp.T + kPartPos - 1) / kPartPos;
+  return (size_t)(tp.nseg() * nparts * D) * (acc_size / 4);
+}
+
+// ---------------------------------------------------------------------------
+// Walker kernel (rows of 16..1024 bytes, whole 16-byte units).  One block per
+// (segment, part of kPartPos walk positions).  A walker is G = row units lanes
+// of one wave, one 16-byte unit each, so a wave instruction moves 64/G rows;
+// a walker owns a contiguous range of the part's positions.
+//   1. The part's sorted keys go to LDS, with run-start flags.
+//   2. Every walker sums the rows of its range from its last run start to the
+//      end (the "tail"; the whole range when it holds no start).
+//   3. A fold over the walkers gives the part's aggregate, which is published
+//      as flagged 64-bit words (the flag says whether the part holds a run
+//      start); the part's carry-in is the sum of the aggregates of the earlier
+//      parts back to the nearest one that holds a start, read newest first.
+//      Only aggregates are combined, in a fixed order, so the rounding does
+//      not depend on timing.
+//   4. Every walker walks its range again with its carry-in and writes the
+//      exclusive (or inclusive) sums, kWalkBatch rows in flight per lane.
+// Parts take per-segment tickets, so a part only waits on parts that running
+// blocks already claimed.
+constexpr int kWalkThreads = 256;
+constexpr int kWalkBatch = 16;
+constexpr int kWalkSpin = 1 << 20;
+
+template <typename Acc>
+struct Pub;
+template <>
+struct Pub<float> {
+  static constexpr int W = 1;  // 64-bit words per value: flag << 32 | bits
+  static __device__ __forceinline__ void put(uint64_t* p, float v, uint32_t flag) {
+    __hip_atomic_store(p, ((uint64_t)flag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // false while the value is not published (or the spin limit ran out)
+  static __device__ __forceinline__ bool get(uint64_t* p, float* v, uint32_t* flag) {
+    uint64_t w = 0;
+    for (int spin = 0; spin < kWalkSpin; ++spin) {
+      w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (w >> 32) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    *v = __uint_as_float((uint32_t)w);
+    *flag = (uint32_t)(w >> 32);
+    return *flag != 0;
+  }
+};
+template <>
+struct Pub<double> {
+  static constexpr int W = 2;  // high half, low half
+  static __device__ __forceinline__ void put(uint64_t* p, double v, uint32_t flag) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    Pub<float>::put(p, __uint_as_float((uint32_t)(b >> 32)), flag);
+    Pub<float>::put(p + 1, __uint_as_float((uint32_t)b), flag);
+  }
+  static __device__ __forceinline__ bool get(uint64_t* p, double* v, uint32_t* flag) {
+    float hi, lo;
+    uint32_t f0, f1;
+    const bool ok = Pub<float>::get(p, &hi, &f0) & Pub<float>::get(p + 1, &lo, &f1);
+    *v = __longlong_as_double(
+        (long long)(((uint64_t)__float_as_uint(hi) << 32) | (uint64_t)__float_as_uint(lo)));
+    *flag = f0;
+    return ok;
+  }
+};
+
+template <int BYTES>
+struct Unit;
+template <>
+struct Unit<16> {
+  using T = u32x4;
+};
+template <>
+struct Unit<8> {
+  using T = u32x2;
+};
+template <>
+struct Unit<4> {
+  using T = uint32_t;
+};
+
+// CPU accumulators -> one output unit (pairs of 16-bit values convert together).
+template <typename XOut, typename StoreF, typename Acc, int CPU>
+__device__ __forceinline__ typename Unit<CPU * (int)sizeof(XOut)>::T pack_unit(const Acc* acc) {
+  using OutV = typename Unit<CPU * (int)sizeof(XOut)>::T;
+  if constexpr (sizeof(XOut) == 2) {
+    union { OutV u; uint32_t w[CPU / 2]; } ov;
+#pragma unroll
+    for (int j = 0; j < CPU / 2; ++j) ov.w[j] = StoreF::store2(acc[2 * j], acc[2 * j + 1]);
+    return ov.u;
+  } else {
+    union { OutV u; XOut e[CPU]; } ov;
+#pragma unroll
+    for (int j = 0; j < CPU; ++j) ov.e[j] = StoreF::store(acc[j]);
+    return ov.u;
+  }
+}
+
+template <typename XIn, typename LoadF, typename Acc, int CPU>
+__device__ __forceinline__ void add_unit(Acc* acc, u32x4 x) {
+  union { u32x4 u; XIn e[CPU]; } cv;
+  cv.u = x;
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) acc[j] += LoadF::load(cv.e[j]);
+}
+
+template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
+__global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
+    const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
+    int tbits, int G, int64_t nparts, XOut* __restrict__ out, uint8_t* __restrict__ omask,
+    uint64_t* __restrict__ status, uint64_t* __restrict__ tickets) {
+  constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
+  using OutV = typename Unit<CPU * (int)sizeof(XOut)>::T;
+  constexpr int NWMAX = kWalkThreads;  // walkers when G == 1
+  __shared__ U kk[kPartPos];
+  __shared__ uint8_t st[kPartPos];
+  __shared__ uint8_t hs[NWMAX];
+  __shared__ Acc tl[kWalkThreads * CPU];  // [walker][column]
+  __shared__ uint32_t s_part;
+  const int tid = threadIdx.x;
+  const int64_t seg = blockIdx.x / nparts;
+  if (tid == 0) s_part = (uint32_t)atomicAdd((unsigned long long*)&tickets[seg], 1ull);
+  __syncthreads();
+  const int64_t q = s_part;
+  if (q >= nparts) return;  // uniform; tickets run 0..nparts-1
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const int64_t segbase = seg * T;
+  const U* sk = sorted + segbase;
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  const int64_t p0 = q * kPartPos;
+  const int n = (int)((T - p0) < kPartPos ? (T - p0) : kPartPos);
+  // 1. keys of walk positions p0 .. p0+n-1 and their run-start flags
+  for (int i = tid; i < n; i += kWalkThreads) {
+    const int64_t wi = p0 + i;
+    kk[i] = sk[REV ? (T - 1 - wi) : wi];
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += kWalkThreads) {
+    const int64_t wi = p0 + i;
+    bool start;
+    if (i > 0) {
+      start = (kk[i] >> tbits) != (kk[i - 1] >> tbits);
+    } else if (wi == 0) {
+      start = true;
+    } else {
+      const U prev = sk[REV ? (T - wi) : (wi - 1)];
+      start = (kk[0] >> tbits) != (prev >> tbits);
+    }
+    st[i] = start ? 1 : 0;
+  }
+  __syncthreads();
+  const int NW = kWalkThreads / G;
+  const int w = tid / G, v = tid - (tid / G) * G;
+  const int len = (n + NW - 1) / NW;
+  const int rs = w * len < n ? w * len : n;
+  const int re = (rs + len) < n ? (rs + len) : n;
+  // Row indices fit in 32 bits (N < 2^31): record (b*T + t)*C + c, or the
+  // sorted position segbase + pos.
+  const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  const int32_t pbase = REV ? (int32_t)(segbase + T - 1 - p0) : (int32_t)(segbase + p0);
+  auto rec_of = [&](int i) -> int32_t { return vbase + (int32_t)(kk[i] & tmask) * Ci; };
+  auto sp_of = [&](int i) -> int32_t { return REV ? pbase - i : pbase + i; };
+  auto irow = [&](int i) -> int32_t { return IN_SORTED ? sp_of(i) : rec_of(i); };
+  auto orow = [&](int i) -> int32_t { return OUT_SORTED ? sp_of(i) : rec_of(i); };
+  const u32x4* inv = (const u32x4*)in;
+  // 2. tail of the walker's range
+  int last = -1;
+  for (int i = rs + v; i < re; i += G)
+    if (st[i]) last = i;
+  for (int o = 1; o < G; o <<= 1) {
+    const int other = __shfl_xor(last, o, kWave);
+    last = other > last ? other : last;
+  }
+  Acc acc[CPU];
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+  for (int i0 = (last >= 0 ? last : rs); i0 < re; i0 += kWalkBatch) {
+    u32x4 x[kWalkBatch];
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
+      x[m] = inv[(int64_t)irow(i) * G + v];
+    }
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m)
+      if (i0 + m < re) add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
+  }
+  if (v == 0) hs[w] = last >= 0 ? 1 : 0;
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) tl[w * (G * CPU) + v * CPU + j] = acc[j];
+  __syncthreads();
+  // 3. part aggregate, look-back over earlier parts, carry-in of every walker
+  const int ncol = G * CPU;  // == D
+  constexpr int PW = Pub<Acc>::W;
+  if (tid < ncol) {
+    Acc run = Acc(0);
+    bool any = false;
+    for (int k = 0; k < NW; ++k) {
+      const Acc t = tl[k * ncol + tid];
+      run = hs[k] ? t : run + t;
+      any = any || hs[k];
+    }
+    uint64_t* sp = status + ((seg * nparts + q) * ncol + tid) * PW;
+    Pub<Acc>::put(sp, run, any ? 2u : 1u);
+    Acc carry = Acc(0);
+    for (int64_t j = q - 1; j >= 0; --j) {
+      Acc val;
+      uint32_t f;
+      if (!Pub<Acc>::get(status + ((seg * nparts + j) * ncol + tid) * PW, &val, &f)) {
+        atomicOr((unsigned long long*)&tickets[gridDim.x / nparts], 1ull);  // error word
+        break;
+      }
+      carry = val + carry;
+      if (f == 2u) break;
+    }
+    for (int k = 0; k < NW; ++k) {
+      const Acc t = tl[k * ncol + tid];
+      tl[k * ncol + tid] = carry;
+      carry = hs[k] ? t : carry + t;
+    }
+  }
+  __syncthreads();
+  // 4. walk with the carry-in and write the sums
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
+  for (int i0 = rs; i0 < re; i0 += kWalkBatch) {
+    u32x4 x[kWalkBatch];
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
+      x[m] = inv[(int64_t)irow(i) * G + v];
+    }
+    OutV* ou = (OutV*)out + v;  // unit v of row r is ou[r * G]
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = i0 + m;
+      if (i < re) {
+        const bool start = st[i] != 0;
+        if (start) {
+#pragma unroll
+          for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+        }
+        const int64_t orw = orow(i);
+        if (!INCL) ou[orw * G] = pack_unit<XOut, StoreF, Acc, CPU>(acc);
+        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
+        if (INCL) ou[orw * G] = pack_unit<XOut, StoreF, Acc, CPU>(acc);
+        if (WMASK && v == 0) omask[orw] = start ? 0 : 1;
+      }
+    }
+  }
+}
+
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
           bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
 hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D, XOut* out,
-                      uint8_t* omask, Acc* tail, uint8_t* flag, Acc* carry, hipStream_t s) {
+                      uint8_t* omask, Acc* tail, uint8_t* flag, Acc* carry, uint64_t* walk,
+                      hipStream_t s) {
+  const int64_t in_bytes = D * (int64_t)sizeof(XIn);
+  const int64_t G = in_bytes / 16;
+  const int out_unit = 16 / (int)sizeof(XIn) * (int)sizeof(XOut);
+  if (walk && in_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
+      ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & (uintptr_t)(out_unit - 1)) == 0 &&
+      tp.T < ((int64_t)1 << 31)) {
+    const int64_t nparts = (tp.T + kPartPos - 1) / kPartPos;
+    const int64_t blocks = tp.nseg() * nparts;
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
+    segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK>
+        <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, (int)G,
+                                                   nparts, out, omask, walk, tickets);
+    return hipGetLastError();
+  }
   const int64_t nch_seg = (tp.T + kChunk - 1) / kChunk;
   const int64_t nchunks = tp.nseg() * nch_seg;
   const int64_t ncb = (D + kWave - 1) / kWave;
@@ -251,28 +527,29 @@ __global__ __launch_bounds__(256) void scatter_reads_kernel(
 template <int DT, typename U>
 hipError_t seg_sum_t(const U* sorted, const void* payload, const Tape& tp, int64_t D, bool direct,
                      void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag, void* carry,
-                     hipStream_t s) {
+                     uint64_t* walk, hipStream_t s) {
   using E = Elem<DT>;
   using S = typename E::store_t;
   using Acc = typename E::acc_t;
   if (direct)
     return run_segsum<U, S, S, Acc, E, E, false, false, false, false, true>(
-        sorted, (const S*)payload, tp, D, (S*)out_or_S, omask, (Acc*)tail, flag, (Acc*)carry, s);
+        sorted, (const S*)payload, tp, D, (S*)out_or_S, omask, (Acc*)tail, flag, (Acc*)carry, walk, s);
   return run_segsum<U, S, S, Acc, E, E, false, false, true, true, false>(
-      sorted, (const S*)payload, tp, D, (S*)out_or_S, nullptr, (Acc*)tail, flag, (Acc*)carry, s);
+      sorted, (const S*)payload, tp, D, (S*)out_or_S, nullptr, (Acc*)tail, flag, (Acc*)carry, walk, s);
 }
 
 template <int DT, typename U>
 hipError_t seg_sum_bwd_t(const U* sorted, const int32_t* spos, const void* grad_out,
                          const Tape& tp, int64_t D, bool direct, void* gacc, void* tail,
-                         uint8_t* flag, void* carry, void* grad_payload, hipStream_t s) {
+                         uint8_t* flag, void* carry, uint64_t* walk, void* grad_payload,
+                         hipStream_t s) {
   using E = Elem<DT>;
   using S = typename E::store_t;
   using Acc = typename E::acc_t;
   if (direct)
     return run_segsum<U, S, S, Acc, E, E, true, false, false, false, false>(
         sorted, (const S*)grad_out, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag,
-        (Acc*)carry, s);
+        (Acc*)carry, walk, s);
   using G = typename std::conditional<DT == kF64, double, float>::type;
   const int64_t N = tp.n();
   hipError_t e = fill_bytes(gacc, 0, (size_t)(N * D) * sizeof(G), s);
@@ -282,7 +559,7 @@ hipError_t seg_sum_bwd_t(const U* sorted, const int32_t* spos, const void* grad_
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   return run_segsum<U, G, S, Acc, In<G, Acc>, E, true, true, true, false, false>(
-      sorted, (const G*)gacc, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag, (Acc*)carry, s);
+      sorted, (const G*)gacc, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag, (Acc*)carry, walk, s);
 }
 
 }  // namespace
@@ -293,15 +570,20 @@ size_t seg_sum_chunks(const Tape& tp) {
 
 size_t acc_bytes(int dtype) { return (dtype == kF32 || dtype == kF64) ? 8 : 4; }
 
+size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype) {
+  // part aggregates, then one ticket per segment and the error word
+  return seg_sum_status_words(tp, D, acc_bytes(dtype)) + (size_t)tp.nseg() + 1;
+}
+
 template <typename U>
 hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& tp, int64_t D,
                    bool direct, void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag,
-                   void* carry, hipStream_t s) {
+                   void* carry, uint64_t* walk, hipStream_t s) {
   switch (dtype) {
-    case kF32: return seg_sum_t<kF32, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, s);
-    case kF64: return seg_sum_t<kF64, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, s);
-    case kBF16: return seg_sum_t<kBF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, s);
-    case kF16: return seg_sum_t<kF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, s);
+    case kF32: return seg_sum_t<kF32, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
+    case kF64: return seg_sum_t<kF64, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
+    case kBF16: return seg_sum_t<kBF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
+    case kF16: return seg_sum_t<kF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -309,25 +591,28 @@ hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& 
 template <typename U>
 hipError_t seg_sum_bwd(const U* sorted, const int32_t* spos, const void* grad_out, int dtype,
                        const Tape& tp, int64_t D, bool direct, float* gacc, void* tail,
-                       uint8_t* flag, void* carry, void* grad_payload, hipStream_t s) {
+                       uint8_t* flag, void* carry, uint64_t* walk, void* grad_payload,
+                       hipStream_t s) {
   switch (dtype) {
-    case kF32: return seg_sum_bwd_t<kF32, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, grad_payload, s);
-    case kF64: return seg_sum_bwd_t<kF64, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, grad_payload, s);
-    case kBF16: return seg_sum_bwd_t<kBF16, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, grad_payload, s);
-    case kF16: return seg_sum_bwd_t<kF16, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, grad_payload, s);
+    case kF32: return seg_sum_bwd_t<kF32, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, walk, grad_payload, s);
+    case kF64: return seg_sum_bwd_t<kF64, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, walk, grad_payload, s);
+    case kBF16: return seg_sum_bwd_t<kBF16, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, walk, grad_payload, s);
+    case kF16: return seg_sum_bwd_t<kF16, U>(sorted, spos, grad_out, tp, D, direct, gacc, tail, flag, carry, walk, grad_payload, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 template hipError_t seg_sum<uint32_t>(const uint32_t*, const void*, int, const Tape&, int64_t, bool,
-                                      void*, uint8_t*, void*, uint8_t*, void*, hipStream_t);
+                                      void*, uint8_t*, void*, uint8_t*, void*, uint64_t*,
+                                      hipStream_t);
 template hipError_t seg_sum<uint64_t>(const uint64_t*, const void*, int, const Tape&, int64_t, bool,
-                                      void*, uint8_t*, void*, uint8_t*, void*, hipStream_t);
+                                      void*, uint8_t*, void*, uint8_t*, void*, uint64_t*,
+                                      hipStream_t);
 template hipError_t seg_sum_bwd<uint32_t>(const uint32_t*, const int32_t*, const void*, int,
                                           const Tape&, int64_t, bool, float*, void*, uint8_t*,
-                                          void*, void*, hipStream_t);
+                                          void*, uint64_t*, void*, hipStream_t);
 template hipError_t seg_sum_bwd<uint64_t>(const uint64_t*, const int32_t*, const void*, int,
                                           const Tape&, int64_t, bool, float*, void*, uint8_t*,
-                                          void*, void*, hipStream_t);
+                                          void*, uint64_t*, void*, hipStream_t);
 
 }  // namespace rem
