@@ -66,43 +66,122 @@ inline RowLayout row_layout(int64_t upr) {
   return RowLayout{tpr, 256 / tpr};
 }
 
+// Slots move kCacheBatch at a time: all loads of a batch are issued before its
+// stores (indices past the end are clamped to a real slot, so every load is
+// unconditional).  The shift runs from the top slot down, batch by batch, so a
+// slot is read before the batch below overwrites it.
+constexpr int kCacheBatch = 8;
+
 template <typename V, typename AT, bool READ>
 __global__ __launch_bounds__(256) void cache_rw_kernel(
     V* __restrict__ values, uint8_t* __restrict__ filled, const AT* __restrict__ raddr,
     const AT* __restrict__ waddr, const V* __restrict__ payload, int64_t BC, int64_t A, int64_t k,
     int64_t upr, int tpr, int gpb, V* __restrict__ out, uint8_t* __restrict__ omask) {
+  constexpr int KB = kCacheBatch;
   const int lid = threadIdx.x % tpr;
   const int64_t bc = (int64_t)blockIdx.x * gpb + threadIdx.x / tpr;
   const bool active = bc < BC;
-  if (READ) {
-    if (active) {
-      const int64_t ar = clamp_addr(raddr, bc, A);
-      for (int64_t j = 0; j < k; ++j) {
-        const int64_t slot = (bc * A + ar) * k + j;
-        const bool f = filled[slot] != 0;
-        for (int64_t v = lid; v < upr; v += tpr) {
-          V val;
-          if (f) {
-            val = values[slot * upr + v];
-          } else {
-            val = V{};
-          }
-          out[(bc * k + j) * upr + v] = val;
+  if (k <= KB && upr <= tpr) {
+    // One round: both addresses, then every load of the step (read slots,
+    // shift sources, payload), then the stores.  A thread owns the same unit
+    // of every row in both halves, and lane 0 of the group owns `filled`.
+    const int64_t s0 = active && READ ? (bc * A + clamp_addr(raddr, bc, A)) * k : 0;
+    const int64_t base = active ? (bc * A + clamp_addr(waddr, bc, A)) * k : 0;
+    const bool mine = active && lid < upr;
+    V rv[KB], sv[KB], pv{};
+    uint8_t rf[KB], sf[KB];
+    if (mine) {
+#pragma unroll
+      for (int m = 0; m < KB; ++m) {
+        const int64_t jr = m < k ? m : k - 1;
+        const int64_t js = (k - 1 - m) >= 1 ? (k - 1 - m) : 1;  // slot js <- js - 1
+        if (READ) rv[m] = values[(s0 + jr) * upr + lid];
+        sv[m] = values[(base + js - 1) * upr + lid];
+        if (READ) rf[m] = filled[s0 + jr];
+        sf[m] = filled[base + js - 1];
+      }
+      pv = payload[bc * upr + lid];
+      if (READ) {
+#pragma unroll
+        for (int m = 0; m < KB; ++m)
+          if (m < k) out[(bc * k + m) * upr + lid] = rf[m] ? rv[m] : V{};
+        if (lid == 0) {
+#pragma unroll
+          for (int m = 0; m < KB; ++m)
+            if (m < k) omask[bc * k + m] = rf[m] ? 1 : 0;
         }
-        if (lid == 0) omask[bc * k + j] = f ? 1 : 0;
       }
     }
-    __syncthreads();  // every read of `filled` precedes the shift below
+    if (READ) __syncthreads();  // every read of the cache precedes the shift below
+    if (!mine) return;
+#pragma unroll
+    for (int m = 0; m < KB; ++m) {
+      const int64_t js = (k - 1 - m) >= 1 ? (k - 1 - m) : 1;
+      if (k > 1) values[(base + js) * upr + lid] = sv[m];
+    }
+    values[base * upr + lid] = pv;
+    if (lid == 0) {
+#pragma unroll
+      for (int m = 0; m < KB; ++m) {
+        const int64_t js = (k - 1 - m) >= 1 ? (k - 1 - m) : 1;
+        if (k > 1) filled[base + js] = sf[m];
+      }
+      filled[base] = 1;
+    }
+    return;
+  }
+  if (READ) {
+    if (active) {
+      const int64_t s0 = (bc * A + clamp_addr(raddr, bc, A)) * k;
+      for (int64_t j0 = 0; j0 < k; j0 += KB) {
+        uint8_t f[KB];
+#pragma unroll
+        for (int m = 0; m < KB; ++m) f[m] = filled[s0 + ((j0 + m) < k ? (j0 + m) : (k - 1))];
+        for (int64_t v = lid; v < upr; v += tpr) {
+          V val[KB];
+#pragma unroll
+          for (int m = 0; m < KB; ++m)
+            val[m] = values[(s0 + ((j0 + m) < k ? (j0 + m) : (k - 1))) * upr + v];
+#pragma unroll
+          for (int m = 0; m < KB; ++m)
+            if (j0 + m < k) out[(bc * k + j0 + m) * upr + v] = f[m] ? val[m] : V{};
+        }
+        if (lid == 0) {
+#pragma unroll
+          for (int m = 0; m < KB; ++m)
+            if (j0 + m < k) omask[bc * k + j0 + m] = f[m] ? 1 : 0;
+        }
+      }
+    }
+    __syncthreads();  // every read of the cache precedes the shift below
   }
   if (!active) return;
-  const int64_t aw = clamp_addr(waddr, bc, A);
-  const int64_t base = (bc * A + aw) * k;
+  const int64_t base = (bc * A + clamp_addr(waddr, bc, A)) * k;
   for (int64_t v = lid; v < upr; v += tpr) {
-    for (int64_t j = k - 1; j > 0; --j) values[(base + j) * upr + v] = values[(base + j - 1) * upr + v];
-    values[base * upr + v] = payload[bc * upr + v];
+    const V pv = payload[bc * upr + v];
+    for (int64_t hi = k - 1; hi >= 1; hi -= KB) {
+      V old[KB];
+#pragma unroll
+      for (int m = 0; m < KB; ++m) {
+        const int64_t j = (hi - m) >= 1 ? (hi - m) : 1;
+        old[m] = values[(base + j - 1) * upr + v];
+      }
+#pragma unroll
+      for (int m = 0; m < KB; ++m) {
+        const int64_t j = (hi - m) >= 1 ? (hi - m) : 1;
+        values[(base + j) * upr + v] = old[m];
+      }
+    }
+    values[base * upr + v] = pv;
   }
   if (lid == 0) {
-    for (int64_t j = k - 1; j > 0; --j) filled[base + j] = filled[base + j - 1];
+    for (int64_t hi = k - 1; hi >= 1; hi -= KB) {
+      uint8_t old[KB];
+#pragma unroll
+      for (int m = 0; m < KB; ++m) old[m] = filled[base + ((hi - m) >= 1 ? (hi - m) : 1) - 1];
+#pragma unroll
+      for (int m = 0; m < KB; ++m) filled[base + ((hi - m) >= 1 ? (hi - m) : 1)] = old[m];
+    }
     filled[base] = 1;
   }
 }

@@ -223,6 +223,100 @@ __global__ __launch_bounds__(256) void search_reads_kernel(
   }
 }
 
+// Reads of one segment against that segment's sorted keys staged in LDS
+// (dynamic, T keys plus padding): one block per (segment, tile of kSearchTile read times);
+// consecutive segments (the heads of one batch row, whose reads share address
+// lines) go to one XCD.  Every thread resolves kSearchIlp reads together with
+// a branchless binary search of log2 steps (lower bound of (a << tbits | t)),
+// so their LDS loads overlap.  Slot j of a read is sorted position
+// lower_bound - 1 - j while the address matches.  Key p sits at LDS word
+// p + p/64: the probes of one search step are lo + step - 1 with lo a multiple
+// of 2*step, which would otherwise all fall in one bank.
+constexpr int kSearchLdsBytes = 64 * 1024;
+constexpr int kSearchTile = 2048;
+constexpr int kSearchIlp = 4;
+
+template <typename U, typename AT>
+__global__ __launch_bounds__(256) void search_lds_kernel(
+    const U* __restrict__ sorted, const AT* __restrict__ raddr, int64_t T, int64_t C, int64_t A,
+    int tbits, int trunc32, int k, int top, int64_t ntile, int64_t nseg,
+    int32_t* __restrict__ src, int32_t* __restrict__ spos) {
+  extern __shared__ __align__(16) unsigned char search_lds[];
+  U* kk = (U*)search_lds;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t seg = lb / ntile;
+  if (seg >= nseg) return;  // padding block of the XCD-rounded grid (uniform)
+  const int tile = (int)(lb - seg * ntile);
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const U* sk = sorted + seg * T;
+  const int Ti = (int)T;
+  // Stage in batches: all 16 loads of a thread are in flight before its stores.
+  for (int i0 = 0; i0 < Ti; i0 += 256 * 16) {
+    U x[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int i = i0 + m * 256 + (int)threadIdx.x;
+      x[m] = i < Ti ? sk[i] : U(0);
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int i = i0 + m * 256 + (int)threadIdx.x;
+      if (i < Ti) kk[i + (i >> 6)] = x[m];
+    }
+  }
+  __syncthreads();
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  const int t0 = tile * kSearchTile;
+  const int nt = (Ti - t0) < kSearchTile ? (Ti - t0) : kSearchTile;
+  const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  for (int base = 0; base < nt; base += 256 * kSearchIlp) {
+    U target[kSearchIlp];
+    int lo[kSearchIlp];
+    int64_t a[kSearchIlp];
+#pragma unroll
+    for (int m = 0; m < kSearchIlp; ++m) {
+      const int tl = base + m * 256 + (int)threadIdx.x;
+      const int t = t0 + (tl < nt ? tl : 0);
+      a[m] = reduce_addr((int64_t)raddr[(b * T + t) * C + c], A, kWrap, trunc32 != 0);
+      target[m] = ((U)a[m] << tbits) | (U)t;
+      lo[m] = 0;
+    }
+    for (int step = top; step > 0; step >>= 1) {
+#pragma unroll
+      for (int m = 0; m < kSearchIlp; ++m) {
+        const int p = lo[m] + step;
+        const int pp = (p <= Ti ? p : Ti) - 1;
+        if (p <= Ti && kk[pp + (pp >> 6)] < target[m]) lo[m] = p;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < kSearchIlp; ++m) {
+      const int tl = base + m * 256 + (int)threadIdx.x;
+      if (tl >= nt) continue;
+      const int64_t r = (b * T + t0 + tl) * C + c;
+      bool alive = true;
+      int32_t first = -1;
+      for (int j = 0; j < k; ++j) {
+        int32_t v = -1;
+        const int q = lo[m] - 1 - j;
+        if (alive && q >= 0) {
+          const U uq = kk[q + (q >> 6)];
+          if ((int64_t)(uq >> tbits) == a[m] && (int64_t)(uq & tmask) < T) {
+            v = vbase + (int32_t)(uq & tmask) * Ci;
+            if (j == 0) first = (int32_t)(seg * T + q);
+          } else {
+            alive = false;
+          }
+        } else {
+          alive = false;
+        }
+        if (src) src[r * k + j] = v;
+      }
+      if (spos) spos[r] = first;
+    }
+  }
+}
+
 // Each thread keeps kIlp independent 16-byte loads in flight (2 measured best
 // at cfg4, against 1, 4 and 8).  src is read once, in order; blocks run in
 // hardware order, which deals consecutive blocks to different XCDs and spreads
@@ -451,6 +545,23 @@ template <typename U>
 hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const Tape& tp, int k,
                         int32_t* src, int32_t* spos, hipStream_t s) {
   const int64_t N = tp.n();
+  if (N == 0) return hipSuccess;
+  const size_t lds = (size_t)(tp.T + tp.T / 64 + 1) * sizeof(U);  // padded: word p + p/64
+  if (lds <= (size_t)kSearchLdsBytes && tp.T < ((int64_t)1 << 30)) {
+    int top = 1;
+    while ((int64_t)top * 2 <= tp.T) top *= 2;  // highest power of two <= T
+    const int64_t ntile = (tp.T + kSearchTile - 1) / kSearchTile;
+    const unsigned g = xcd_grid(tp.nseg() * ntile, 1, (int64_t)1 << 31);
+    if (addr64)
+      search_lds_kernel<U, int64_t><<<g, 256, lds, s>>>(sorted, (const int64_t*)raddr, tp.T, tp.C,
+                                                        tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k,
+                                                        top, ntile, tp.nseg(), src, spos);
+    else
+      search_lds_kernel<U, int32_t><<<g, 256, lds, s>>>(sorted, (const int32_t*)raddr, tp.T, tp.C,
+                                                        tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k,
+                                                        top, ntile, tp.nseg(), src, spos);
+    return hipGetLastError();
+  }
   const unsigned grid = grid_for(N, 256);
   if (addr64)
     search_reads_kernel<U, int64_t><<<grid, 256, 0, s>>>(sorted, (const int64_t*)raddr, N, tp.T,
