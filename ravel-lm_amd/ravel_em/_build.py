@@ -44,7 +44,8 @@ def build(verbose: bool = False) -> str:
             if verbose and msg:
                 print(msg, file=sys.stderr)
     tmp = out + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    # --no-undefined: a missing definition fails the build, not the first dlopen
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp, *objs])
     os.replace(tmp, out)
     return out
 
