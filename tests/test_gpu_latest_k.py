@@ -121,6 +121,42 @@ SMALL = [
 ]
 
 
+# k == 1 self-links: the link's segment-major sources go through the
+# vectorized transpose when the head count is a power of two (up to 16) and
+# through the generic one otherwise; the gather then picks its unit from the
+# row width and alignment.  Cover several head counts and row widths, ragged
+# time tiles, and an unaligned payload view (2-byte units).
+LINK1_SHAPES = [
+    # B, T, C, D, dtype
+    (2, 37, 2, 8, torch.bfloat16),    # 16-byte rows
+    (1, 300, 4, 16, torch.float32),   # 64-byte rows
+    (3, 129, 8, 64, torch.bfloat16),  # 128-byte rows (the headline shape's rows)
+    (2, 50, 16, 128, torch.float32),  # 512-byte rows
+    (1, 1000, 16, 4, torch.float32),  # 16-byte rows, 16 heads
+    (2, 70, 4, 8, torch.float64),     # 64-byte rows of float64
+    (2, 90, 3, 8, torch.bfloat16),    # 3 heads: the generic transpose
+    (1, 80, 32, 8, torch.bfloat16),   # 32 heads: the generic transpose
+]
+
+
+@pytest.mark.parametrize("case", LINK1_SHAPES, ids=[str(i) for i in range(len(LINK1_SHAPES))])
+def test_latest_1_shapes(device, case):
+    B, T, C, D, dtype = case
+    g = torch.Generator().manual_seed(T * 7 + C)
+    w = torch.randint(0, 40, (B, T, C), generator=g)
+    p = torch.randn(B, T, C, D, generator=g).to(dtype)
+    check_against_oracle(w.to(device), p.to(device), A=40, k=1)
+
+
+def test_latest_1_unaligned_payload_view(device):
+    g = torch.Generator().manual_seed(5)
+    w = torch.randint(0, 9, (2, 33, 4), generator=g)
+    base = torch.randn(2 * 33 * 4 * 8 + 1, generator=g).to(torch.bfloat16).to(device)
+    p = base[1:].view(2, 33, 4, 8)  # 2-byte offset: 16-byte rows, unaligned on the device
+    assert p.data_ptr() % 16 != 0
+    check_against_oracle(w.to(device), p, A=9, k=1)
+
+
 @pytest.mark.parametrize("case", SMALL, ids=[str(i) for i in range(len(SMALL))])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_latest_k_parity(device, case, dtype):
