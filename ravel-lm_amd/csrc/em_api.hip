@@ -149,12 +149,13 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s,
+                              nullptr, 0, link && k == 1 ? src_seg : nullptr);
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   stage_begin(kStageResolve, s);
   if (link) {
-    e = link_same<U>(sorted, tp, (int)k, src_seg, s);
+    if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
@@ -177,10 +178,11 @@ int resolve_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s);
+  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s,
+                              nullptr, 0, link && k == 1 ? src_seg : nullptr);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (link) {
-    e = link_same<U>(sorted, tp, (int)k, src_seg, s);
+    if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
     e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);

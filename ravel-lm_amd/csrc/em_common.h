@@ -166,10 +166,14 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, u
 // Sort every segment of the tape by packed key.  Returns the buffer (ka or kb)
 // holding the sorted keys in *sorted.  The zero_words words at `zero` are set
 // to zero on the way (state that a later kernel of the same call needs clear).
+// With link_seg (read == write, k == 1), the sort may fuse the self-link into
+// its last pass: it then writes the segment-major sources [B,C,T] to link_seg,
+// no sorted keys, and sets *sorted to nullptr.
 template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp,
                      U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s,
-                     uint32_t* zero = nullptr, int64_t zero_words = 0);
+                     uint32_t* zero = nullptr, int64_t zero_words = 0,
+                     int32_t* link_seg = nullptr);
 size_t sort_counts_words(const Tape& tp);
 size_t sort_fused_words(const Tape& tp, size_t key_bytes);
 

@@ -634,6 +634,131 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
 }
 
+// The last pass fused with the read == write, k == 1 link (32-bit keys).  The
+// look-back words are 64-bit and carry, besides the digit count, the last key
+// of the digit among the tiles they cover:
+//   bits 63..62 flag (A aggregate / P inclusive), bit 61 "has a key",
+//   bits 60..32 count, bits 31..0 the key.
+// After the pass, the key at local sorted index idx of digit d has as global
+// predecessor stage[idx - 1] inside its digit's run, or for the run's first key
+// the last digit-d key of the earlier tiles (a key of another digit has another
+// address and never links).  The tile writes src_seg[seg][t] =
+// (b*T + t')*C + c for a same-address predecessor t', else -1: random 4-byte
+// writes inside the segment's T-word region, which stays in one XCD's L2.
+constexpr uint64_t kLFlagA = 1ull << 62;
+constexpr uint64_t kLFlagP = 2ull << 62;
+constexpr uint64_t kLHasKey = 1ull << 61;
+constexpr uint64_t kLCountMask = (1ull << 29) - 1;
+
+template <int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
+    const uint32_t* __restrict__ in, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ ticket, int64_t T, int64_t C, int ntiles, int64_t nblk, int shift,
+    int tbits, uint32_t* __restrict__ err, int32_t* __restrict__ src_seg) {
+  using U = uint32_t;
+  constexpr int NW = kSortThreads / kWave;
+  constexpr int TILE = kSortThreads * ITEMS;
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ uint32_t s_ticket;
+  __shared__ uint32_t carry_key[kRadix];
+  __shared__ uint8_t carry_has[kRadix];
+  __shared__ U stage[TILE];
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  const int64_t seg = lb / ntiles;
+  if (tid == 0) s_ticket = atomicAdd(&ticket[seg], 1u);
+  __syncthreads();
+  const int tile = (int)s_ticket;
+  if (tile >= ntiles) return;  // uniform per block; tickets run 0..ntiles-1
+  const int64_t start = (int64_t)tile * TILE;
+  const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  U key[ITEMS];
+  load_tile<U, ITEMS>(in + seg * T + start, n, key);
+  uint32_t rank[ITEMS];
+  uint32_t own;
+  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  __syncthreads();  // dstart of every digit
+  // The tile in local sorted order (digit runs in order).
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = w * kWave * ITEMS + i * kWave + lane;
+    if (idx < n) {
+      const uint32_t d = (key[i] >> shift) & (kRadix - 1);
+      stage[dstart[d] + wcnt[w][d] + rank[i]] = key[i];
+    }
+  }
+  __syncthreads();
+  const uint32_t own_last = own ? stage[dstart[tid] + own - 1] : 0u;
+  uint64_t* st = status + (seg * ntiles) * (int64_t)kRadix;
+  const uint64_t agg = (own ? (kLHasKey | own_last) : 0ull) | ((uint64_t)own << 32);
+  __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], (tile == 0 ? kLFlagP : kLFlagA) | agg,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t excl = 0, lastk = 0;
+  bool found = false, ok = true, done = tile == 0;
+  for (int hi = tile - 1; !done && hi >= 0; hi -= kLookBatch) {
+    uint64_t v[kLookBatch];
+#pragma unroll
+    for (int j = 0; j < kLookBatch; ++j)
+      v[j] = (hi - j >= 0) ? __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : kLFlagP;
+#pragma unroll
+    for (int j = 0; j < kLookBatch; ++j) {
+      if (done || hi - j < 0) continue;
+      uint64_t x = v[j];
+      int spins = 0;
+      while ((x >> 62) == 0 && spins < kSpinLimit) {
+        __builtin_amdgcn_s_sleep(1);
+        x = __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        ++spins;
+      }
+      if ((x >> 62) == 0) {
+        ok = false;
+        done = true;
+        continue;
+      }
+      excl += (uint32_t)((x >> 32) & kLCountMask);
+      if (!found && (x & kLHasKey)) {
+        found = true;
+        lastk = (uint32_t)x;
+      }
+      if ((x >> 62) == 2) done = true;
+    }
+  }
+  if (!ok) atomicOr(err, 1u);
+  if (tile > 0) {
+    const bool has = own || found;
+    const uint64_t inc = (has ? kLHasKey : 0ull) | (uint64_t)(own ? own_last : lastk) |
+                         ((uint64_t)((excl + own) & (uint32_t)kLCountMask) << 32);
+    __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kLFlagP | inc, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  carry_key[tid] = lastk;
+  carry_has[tid] = found ? 1 : 0;
+  __syncthreads();
+  const U tmask = (U)((1u << tbits) - 1u);
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  int32_t* dst = src_seg + seg * T;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = i * kSortThreads + tid;
+    if (idx < n) {
+      const U u = stage[idx];
+      const uint32_t d = (u >> shift) & (kRadix - 1);
+      const bool inrun = idx > (int)dstart[d];
+      const U pk = inrun ? stage[idx - 1] : carry_key[d];
+      const bool has = inrun || carry_has[d] != 0;
+      const int32_t v = (has && (pk >> tbits) == (u >> tbits)) ? vbase + (int32_t)(pk & tmask) * Ci : -1;
+      dst[u & tmask] = v;
+    }
+  }
+}
+
 int pack_tt(int64_t C, size_t key_bytes) {
   int tt = kPackTT;
   while (tt > 1 && (size_t)C * (size_t)(tt + 1) * key_bytes > 48 * 1024) tt >>= 1;
@@ -691,13 +816,15 @@ size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
   const int64_t offs = tp.nseg() * scatter0_tiles(tp) * kRadix;
   const int64_t bins = tp.nseg() * npass * kRadix;
   const int64_t status = tp.nseg() * sweep_tiles(tp) * kRadix;
-  return (size_t)(hist + offs + bins + 2 * status + (npass + 1) * tp.nseg());
+  // two look-back status buffers, each room for one 64-bit word per entry
+  return (size_t)(hist + offs + bins + 4 * status + (npass + 1) * tp.nseg());
 }
 
 template <typename U>
 static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* wmask,
                                   const Tape& tp, PackPlan pl, U* ka, U* kb, uint32_t* words,
-                                  U** sorted, hipStream_t s, uint32_t* zero, int64_t zero_words) {
+                                  U** sorted, hipStream_t s, uint32_t* zero, int64_t zero_words,
+                                  int32_t* link_seg) {
   const int tt = pl.TT;
   const int ncg = (int)((tp.C + pl.CC - 1) / pl.CC);
   const int npass = (tp.abits + 7) / 8;
@@ -708,7 +835,8 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   const int64_t offs_words = tp.nseg() * nsct * kRadix;
   const int64_t bin_words = tp.nseg() * npass * kRadix;
   const int nts = (int)sweep_tiles(tp);
-  const int64_t status_words = tp.nseg() * nts * kRadix;
+  const int64_t entries = tp.nseg() * nts * kRadix;  // look-back entries of one pass
+  const int64_t status_words = 2 * entries;           // a buffer holds 64-bit entries
   uint32_t* hist = words;
   uint32_t* offs = hist + hist_words;
   uint32_t* binbase = offs + offs_words;
@@ -750,8 +878,20 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   U* alt = ka;
   const int64_t nblks = tp.nseg() * nts;
   const unsigned gs = xcd_grid(nblks, 1, (int64_t)1 << 31);
+  // With link_seg, the last pass (32-bit keys, at least two passes) also
+  // links every record to its same-address predecessor and writes no keys.
+  const bool fuse_link = link_seg && sizeof(U) == 4 && npass >= 2;
   for (int p = 1; p < npass; ++p) {
     uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
+    if (fuse_link && p == npass - 1) {
+      sweep_link_kernel<kSweepItems><<<gs, kSortThreads, 0, s>>>(
+          (const uint32_t*)cur, (uint64_t*)status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T,
+          tp.C, nts, nblks, tp.tbits + 8 * p, tp.tbits, err, link_seg);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      *sorted = nullptr;
+      return hipSuccess;
+    }
     sweep_kernel<U, kSweepItems><<<gs, kSortThreads, 0, s>>>(
         cur, alt, binbase + p * kRadix, npass,
         status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts, nblks, tp.tbits + 8 * p, next,
@@ -769,12 +909,12 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
 template <typename U>
 hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp, U* ka,
                      U* kb, uint32_t* counts, U** sorted, hipStream_t s, uint32_t* zero,
-                     int64_t zero_words) {
+                     int64_t zero_words, int32_t* link_seg) {
   if (tp.fused) {
     const PackPlan pl = fused_plan(tp, sizeof(U));
     if (pl.TT)
       return sort_tape_fused<U>(addr, addr64, wmask, tp, pl, ka, kb, counts, sorted, s, zero,
-                                zero_words);
+                                zero_words, link_seg);
   }
   if (zero && zero_words > 0) {
     const hipError_t ez = fill_bytes(zero, 0, (size_t)zero_words * 4, s);
@@ -835,10 +975,10 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 
 template hipError_t sort_tape<uint32_t>(const void*, bool, const uint8_t*, const Tape&, uint32_t*,
                                         uint32_t*, uint32_t*, uint32_t**, hipStream_t, uint32_t*,
-                                        int64_t);
+                                        int64_t, int32_t*);
 template hipError_t sort_tape<uint64_t>(const void*, bool, const uint8_t*, const Tape&, uint64_t*,
                                         uint64_t*, uint32_t*, uint64_t**, hipStream_t, uint32_t*,
-                                        int64_t);
+                                        int64_t, int32_t*);
 template hipError_t emit_order<uint32_t>(const uint32_t*, const uint8_t*, int64_t*, const Tape&,
                                          void*, bool, int64_t*, hipStream_t);
 template hipError_t emit_order<uint64_t>(const uint64_t*, const uint8_t*, int64_t*, const Tape&,

@@ -148,6 +148,31 @@ def test_latest_1_shapes(device, case):
     check_against_oracle(w.to(device), p.to(device), A=40, k=1)
 
 
+# Self-links with k == 1, no mask, 32-bit keys and two or more digit passes
+# (A > 256) are linked inside the sort's last pass: cover one and many tiles
+# per segment, three passes, long runs of one hot address, and the sources.
+FUSED_LINK = [
+    # B, T, C, A, hot fraction
+    (2, 300, 3, 257, 0.0),
+    (2, 5000, 4, 1000, 0.0),
+    (1, 65536, 2, 65536, 0.0),
+    (1, 30000, 3, 1 << 17, 0.0),   # 3 passes (17 + 15 bits)
+    (2, 20000, 2, 4096, 0.9),      # one hot address: runs across all tiles
+    (1, 9000, 16, 70000, 0.5),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_LINK, ids=[str(i) for i in range(len(FUSED_LINK))])
+def test_latest_1_link_in_sort(device, case):
+    B, T, C, A, hot = case
+    g = torch.Generator().manual_seed(B * 131 + T + C)
+    w = torch.randint(0, A, (B, T, C), generator=g)
+    if hot > 0:
+        w = torch.where(torch.rand(B, T, C, generator=g) < hot, torch.full_like(w, 7), w)
+    p = torch.randn(B, T, C, 8, generator=g).to(torch.bfloat16)
+    check_against_oracle(w.to(device), p.to(device), A=A, k=1)
+
+
 def test_latest_1_unaligned_payload_view(device):
     g = torch.Generator().manual_seed(5)
     w = torch.randint(0, 9, (2, 33, 4), generator=g)
