@@ -88,6 +88,63 @@ def cpu_baseline(w, budget_s):
     }
 
 
+def suite_cpu_baseline(w, op, budget_s=6.0):
+    """The reference CPU path (torch restatement) on one suite workload and op."""
+    import torch
+
+    from oracle import torch_ref
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+
+    def timed(fn, reps):
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < reps and (not times or time.perf_counter() - t_start < budget_s):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    if op in ("latest_k", "seg_sum"):
+        write = w.write.cpu()
+        read = None if w.read is None else w.read.cpu()
+        payload = w.payload.cpu()
+        B, T = write.shape[:2]
+        if op == "latest_k":
+            fn = lambda: torch_ref.latest_k(write, payload, read, address_space=w.address_space, k=w.k)
+        else:
+            fn = lambda: torch_ref.seg_sum(write, payload, read, address_space=w.address_space)
+        med, n = timed(fn, 3)
+        return {"value": B * T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{n} full calls, median {med:.4f} s"}
+    # cfg5: the reference cache is the k = 1 one, written token by token
+    # (ravel_lm/model.py:600-602) and read/written once per decode step.
+    pw, pp = w.prefill_write.cpu(), w.prefill_payload.cpu()
+    B, T, H = pw.shape
+    D = pp.shape[-1]
+    values = torch.zeros(B, H, w.address_space, D, dtype=pp.dtype)
+    filled = torch.zeros(B, H, w.address_space, dtype=torch.bool)
+    if op == "prefill":
+        n_tok = min(T, 64)
+        t0 = time.perf_counter()
+        for t in range(n_tok):
+            torch_ref.cache_write(values, filled, pw[:, t], pp[:, t])
+        per_tok = (time.perf_counter() - t0) / n_tok
+        return {"value": B / per_tok, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{n_tok} of {T} prefill tokens written one at a time (k=1 cache)"}
+    sr, sw, sp = w.step_read.cpu(), w.step_write.cpu(), w.step_payload.cpu()
+    n_steps = min(sr.shape[0], 128)
+    t0 = time.perf_counter()
+    for s in range(n_steps):
+        torch_ref.cache_read(values, filled, sr[s])
+        torch_ref.cache_write(values, filled, sw[s], sp[s])
+    per_step = (time.perf_counter() - t0) / n_steps
+    return {"value": B / per_step, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_steps} decode steps, read then write (k=1 cache)"}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -106,7 +163,7 @@ def main():
     if args.suite:
         from ravel_em import suite
 
-        suite.run(dev)
+        suite.run(dev, cpu=None if args.no_cpu_baseline else suite_cpu_baseline)
         return
     log("generating cfg4 inputs on the device")
     w = workloads.cfg4(dev, adversarial=args.adversarial)

@@ -11,14 +11,15 @@ line per measurement:
 Each op is timed with HIP events around every call on torch's current stream
 (warmup first, then the median of the calls).  Bytes are the algorithmic bytes
 of the call (inputs read once plus outputs written once), and ``frac`` is the
-achieved rate over 8 TB/s.
+achieved rate over 8 TB/s.  A caller may pass ``cpu(workload, op)``, which
+returns a CPU-baseline dict for the same inputs; it is added to each line.
 """
 from __future__ import annotations
 
 import json
 import statistics
 import sys
-from typing import Callable, List
+from typing import Callable, List, Optional
 
 import torch
 
@@ -53,7 +54,7 @@ def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) ->
     return out
 
 
-def tape_lines(w: workloads.Workload, iters: int) -> List[dict]:
+def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None) -> List[dict]:
     B, T, C, D = w.shape
     lines = []
     us = statistics.median(time_calls(
@@ -69,10 +70,14 @@ def tape_lines(w: workloads.Workload, iters: int) -> List[dict]:
     addr = N * w.write.element_size() * (1 if w.read is None else 2)
     sum_bytes = addr + N * D * esz + N * D * esz + N
     lines.append(_line(w.name, "seg_sum", us, sum_bytes, B * T, shape=[B, T, C, D], A=w.address_space))
+    if cpu is not None:
+        for line in lines:
+            line["cpu_baseline"] = cpu(w, line["op"])
     return lines
 
 
-def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128) -> List[dict]:
+def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
+                 cpu: Optional[Callable] = None) -> List[dict]:
     w = workloads.cfg5(dev, steps=steps)
     B, T, H = w.prefill_write.shape
     D = w.prefill_payload.shape[-1]
@@ -121,10 +126,13 @@ def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128) -
     us = statistics.median(t) / steps
     lines.append(_line("cfg5", "decode_step_graph", us, step_bytes, B, steps=steps,
                        steps_per_s=1e6 / us, graph_steps=graph_chunk))
+    if cpu is not None:
+        for line in lines:
+            line["cpu_baseline"] = cpu(w, line["op"])
     return lines
 
 
-def run(dev: torch.device, iters: int = 50) -> List[dict]:
+def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None) -> List[dict]:
     lines: List[dict] = []
     tapes = [
         lambda: workloads.cfg1(dev, "1"),
@@ -137,12 +145,12 @@ def run(dev: torch.device, iters: int = 50) -> List[dict]:
     ]
     for make in tapes:
         w = make()
-        for line in tape_lines(w, iters):
+        for line in tape_lines(w, iters, cpu):
             print(json.dumps(line), flush=True)
             lines.append(line)
         del w
         torch.cuda.empty_cache()
-    for line in decode_lines(dev):
+    for line in decode_lines(dev, cpu=cpu):
         print(json.dumps(line), flush=True)
         lines.append(line)
     return lines
