@@ -122,6 +122,28 @@ int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, con
                          int64_t n_rows, void* out_values, uint8_t* out_mask, void* stream);
 
 /*
+ * The latest-1 lookup fused into the fuse layer's linear map: the reference's
+ * fused arm triton_fused_latest1_linear (ravel_lm/triton_memory.py:477-485, its
+ * autograd forward :378-426), called from ravel_lm/model.py:350-365.
+ *   out[b,t,m] = sum_{c,p} values[b,t,c,p] * weight[m, c*P + p]
+ * with values the latest-1 lookup of causal_last_k_lookup(write, payload,
+ * read, k=1) (zero rows where nothing was written).  The looked-up rows are
+ * gathered straight into the GEMM's MFMA tiles and never stored.  read_addr
+ * may be null (reads == writes).  payload [B,T,C,P] and weight [M, C*P] are
+ * bf16 or f16 (the same dtype); out [B,T,M] is that dtype, accumulated in fp32.
+ * Needs P % 8 == 0, M % 8 == 0, M <= 256 and 16-byte aligned payload, weight
+ * and out (RAVEL_EM_EINVAL otherwise).  out_src (optional) receives the int32
+ * sources [B,T,C] (-1 = zero row) that the backward needs.
+ */
+size_t ravel_em_latest1_linear_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
+                                         int has_read, int want_src);
+int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                                const void* payload, int payload_dtype, const void* weight,
+                                int64_t B, int64_t T, int64_t C, int64_t P, int64_t M, int64_t A,
+                                void* out, int32_t* out_src, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * Backward of causal_last_k_lookup (autograd of ravel_memory.py:173-175;
  * GPU arm triton_latest1.py:132-142): grad_payload[src] += grad_values.
  * `chain` = 1 selects the deterministic successor-chain kernel, valid only when

@@ -500,6 +500,56 @@ int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int
                                workspace_bytes, s);
 }
 
+size_t ravel_em_latest1_linear_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
+                                         int has_read, int want_src) {
+  if (check_tape(B, T, C, A)) return 0;
+  size_t bytes = ravel_em_latest_k_resolve_workspace(B, T, C, A, 1, has_read, 0);
+  if (!want_src) bytes = (bytes + 255) / 256 * 256 + (size_t)(B * T * C) * sizeof(int32_t);
+  return bytes;
+}
+
+int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                                const void* payload, int payload_dtype, const void* weight,
+                                int64_t B, int64_t T, int64_t C, int64_t P, int64_t M, int64_t A,
+                                void* out, int32_t* out_src, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (payload_dtype != kBF16 && payload_dtype != kF16)
+    return fail(RAVEL_EM_EINVAL, "the fused latest-1 linear takes bf16 or f16 payloads (got %d)",
+                payload_dtype);
+  if (P < 1 || M < 1) return fail(RAVEL_EM_EINVAL, "P and M must be positive");
+  if (!gather_gemm_apply(payload_dtype, P, M, payload, weight, out))
+    return fail(RAVEL_EM_EINVAL,
+                "the fused latest-1 linear needs P %% 8 == 0, M %% 8 == 0, M <= 256 and 16-byte "
+                "aligned payload, weight and output (P=%lld M=%lld)",
+                (long long)P, (long long)M);
+  if (B * T * C == 0) return RAVEL_EM_OK;
+  if (!write_addr || !payload || !weight || !out) return fail(RAVEL_EM_EINVAL, "null pointer");
+  // Sources: into out_src when given, else at the end of the workspace.
+  const size_t rws = ravel_em_latest_k_resolve_workspace(B, T, C, A, 1, read_addr != nullptr, 0);
+  int32_t* src = out_src;
+  if (!src) {
+    const size_t off = (rws + 255) / 256 * 256;
+    if (workspace_bytes < off + (size_t)(B * T * C) * sizeof(int32_t))
+      return fail(RAVEL_EM_EWORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes,
+                  off + (size_t)(B * T * C) * sizeof(int32_t));
+    src = (int32_t*)((char*)workspace + off);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  stage_begin(kStageResolve, s);
+  int rc = ravel_em_latest_k_resolve(write_addr, read_addr, addr_dtype, nullptr, B, T, C, A, 1, src,
+                                     workspace, workspace_bytes, stream);
+  stage_end(kStageResolve, s);
+  if (rc != RAVEL_EM_OK) return rc;
+  stage_begin(kStageGather, s);
+  hipError_t e = gather_gemm(payload, src, weight, payload_dtype, B * T, C, P, M, out, s);
+  stage_end(kStageGather, s);
+  if (e != hipSuccess) return hip_fail(e, "gather-GEMM");
+  return RAVEL_EM_OK;
+}
+
 int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, const int32_t* src,
                          int64_t n_rows, void* out_values, uint8_t* out_mask, void* stream) {
   g_err.clear();

@@ -194,6 +194,14 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
 // out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s);
+// out[n, m] = sum_k A[n, k] W[m, k] with A gathered through record-major k == 1
+// sources (n = b*T + t, k = c*P + p); 16-bit payloads (bf16/f16), W [M][C*P] of
+// the same dtype, out [NR][M].  gather_gemm_apply says whether the MFMA kernel
+// takes the shape (P % 8 == 0, M % 8 == 0, M <= 256, 16-byte aligned).
+bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, const void* W,
+                       const void* out);
+hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, int dtype,
+                       int64_t NR, int64_t C, int64_t P, int64_t M, void* out, hipStream_t s);
 // Segment-major sources -> record-major (a no-op layout change when C == 1).
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
                             hipStream_t s);

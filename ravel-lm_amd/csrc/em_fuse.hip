@@ -1,0 +1,193 @@
+// Latest-1 lookup fused into the fuse layer's linear map (gfx950 MFMA).
+//
+// Replaces the reference's fused arm triton_fused_latest1_linear
+// (ravel_lm/triton_memory.py:378-426, :477-485), called from
+// ravel_lm/model.py:350-365: out[b,t,:] = W @ concat_c(values[b,t,c,:]) with
+// values the latest-1 lookup.  The [B*T, C*P] matrix of looked-up rows never
+// exists in memory: the GEMM's A operand is gathered straight from the payload
+// through the sources (src[b,t,c] = record of the value, -1 = zero row).
+//
+//   out[n, m] = sum_k A[n, k] * W[m, k],   n = b*T + t, k = c*P + p,
+//   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
+//
+// Tiles: a block computes kRows rows x kCols (= 4 waves x 64) columns over K in
+// chunks of kChunk.  A chunk's A tile is gathered in 16-byte units (8 values;
+// P % 8 == 0 keeps a unit inside one head), W's tile is read row-major, both
+// go to LDS with rows padded to kLds elements (144 bytes: the 16 rows that one
+// MFMA operand read touches land in distinct banks).  Wave w owns columns
+// [64w, 64w + 64) and all kRows rows: (kRows/16) x 4 tiles of
+// v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to the
+// payload dtype.  Operand lane layout (checked on the device): A lane l holds
+// row l%16, k (l/16)*8 .. +7; B lane l holds column l%16, the same k; the
+// result lane l holds column l%16, rows (l/16)*4 .. +3.  The epilogue stages
+// the tile in LDS and writes whole 16-byte units of the output rows.
+
+#include "em_common.h"
+
+namespace rem {
+
+namespace {
+
+constexpr int kRows = 128;
+constexpr int kCols = 256;
+constexpr int kChunk = 64;
+constexpr int kLds = kChunk + 8;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v_t __attribute__((ext_vector_type(2)));
+
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <bool F16>
+__device__ __forceinline__ uint16_t round16(float x) {
+  const f32x2v_t v = {x, 0.0f};
+  if constexpr (F16)
+    return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2v_t));
+  else
+    return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void gather_gemm_kernel(
+    const uint16_t* __restrict__ payload, const int32_t* __restrict__ src,
+    const uint16_t* __restrict__ W, int64_t NR, int C, int P, int M, int64_t nsrc,
+    uint16_t* __restrict__ out) {
+  constexpr int RT = kRows / 16;  // row tiles per wave
+  __shared__ __align__(16) uint16_t As[kRows * kLds];
+  __shared__ __align__(16) uint16_t Bs[kCols * kLds];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t row0 = (int64_t)blockIdx.x * kRows;
+  const int K = C * P;
+  f32x4_t acc[RT][4];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool wave_live = wave * 64 < M;  // columns past M are padding
+  // The next chunk's tiles are loaded into registers while the current chunk
+  // multiplies out of LDS.
+  constexpr int AU = kRows * 8 / 256;
+  constexpr int BU = kCols * 8 / 256;
+  u32x4 av[AU], bv[BU];
+  auto load_chunk = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < AU; ++q) {
+      const int u = tid + 256 * q;
+      const int r = u >> 3, piece = u & 7;
+      const int k = k0 + piece * 8;
+      const int64_t n = row0 + r;
+      av[q] = u32x4{0u, 0u, 0u, 0u};
+      if (n < NR && k < K) {
+        const int c = k / P;
+        const int32_t s = src[n * C + c];
+        if (s >= 0 && s < nsrc) av[q] = *(const u32x4*)(payload + (int64_t)s * P + (k - c * P));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < BU; ++q) {
+      const int u = tid + 256 * q;
+      const int m = u >> 3, piece = u & 7;
+      const int k = k0 + piece * 8;
+      bv[q] = (m < M && k < K) ? *(const u32x4*)(W + (int64_t)m * K + k) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  load_chunk(0);
+  for (int k0 = 0; k0 < K; k0 += kChunk) {
+#pragma unroll
+    for (int q = 0; q < AU; ++q) {
+      const int u = tid + 256 * q;
+      *(u32x4*)&As[(u >> 3) * kLds + (u & 7) * 8] = av[q];
+    }
+#pragma unroll
+    for (int q = 0; q < BU; ++q) {
+      const int u = tid + 256 * q;
+      *(u32x4*)&Bs[(u >> 3) * kLds + (u & 7) * 8] = bv[q];
+    }
+    __syncthreads();
+    if (k0 + kChunk < K) load_chunk(k0 + kChunk);
+    if (wave_live) {
+#pragma unroll
+      for (int ks = 0; ks < kChunk / 32; ++ks) {
+        const int kk = ks * 32 + (lane >> 4) * 8;
+        u32x4 b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          b[j] = *(const u32x4*)&Bs[(wave * 64 + j * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const u32x4 a = *(const u32x4*)&As[(i * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // Epilogue: round to 16 bits and stage the tile in the (now free) B buffer,
+  // kRows/2 rows at a time (padded rows of kCols + 8), then write 16-byte units.
+  uint16_t* Cs = Bs;
+  constexpr int CSTRIDE = kCols + 8;
+  static_assert(kRows / 2 * CSTRIDE <= kCols * kLds, "epilogue half-tile must fit the B buffer");
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    if (wave_live) {
+#pragma unroll
+      for (int i = half * RT / 2; i < (half + 1) * RT / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = i * 16 + (lane >> 4) * 4 + e - half * (kRows / 2);
+            const int col = wave * 64 + j * 16 + (lane & 15);
+            Cs[r * CSTRIDE + col] = round16<F16>(acc[i][j][e]);
+          }
+    }
+    __syncthreads();
+    const int upr = M >> 3;  // 16-byte units per output row (M % 8 == 0)
+    for (int u = tid; u < (kRows / 2) * upr; u += 256) {
+      const int r = u / upr, piece = u - (u / upr) * upr;
+      const int64_t n = row0 + half * (kRows / 2) + r;
+      if (n < NR) *(u32x4*)(out + n * M + piece * 8) = *(const u32x4*)&Cs[r * CSTRIDE + piece * 8];
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, const void* W,
+                       const void* out) {
+  return (dtype == kBF16 || dtype == kF16) && P % 8 == 0 && M >= 8 && M <= kCols && M % 8 == 0 &&
+         (((uintptr_t)payload | (uintptr_t)W | (uintptr_t)out) & 15) == 0;
+}
+
+hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, int dtype,
+                       int64_t NR, int64_t C, int64_t P, int64_t M, void* out, hipStream_t s) {
+  if (NR == 0) return hipSuccess;
+  const int64_t blocks = (NR + kRows - 1) / kRows;
+  if (blocks > INT32_MAX || C * P > INT32_MAX) return hipErrorInvalidValue;
+  const int64_t nsrc = NR * C;
+  if (dtype == kF16)
+    gather_gemm_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(
+        (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
+        (uint16_t*)out);
+  else
+    gather_gemm_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(
+        (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
+        (uint16_t*)out);
+  return hipGetLastError();
+}
+
+}  // namespace rem

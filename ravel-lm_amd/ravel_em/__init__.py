@@ -2,8 +2,11 @@
 
 Drop-in for the reference module ``ravel_lm/ravel_memory.py``: the public
 functions below keep its names and signatures and run as hand-written HIP
-kernels for gfx950 behind the C ABI in include/ravel_em.h.
+kernels for gfx950 behind the C ABI in include/ravel_em.h.  ``fused_latest1_linear``
+replaces the reference's fused arm ``triton_fused_latest1_linear``
+(ravel_lm/triton_memory.py:477-485).
 """
+from .fused import fused_latest1_linear
 from .ravel_memory import (
     RavelLayerCache,
     _composite_key_dtype,
@@ -19,5 +22,6 @@ __all__ = [
     "causal_last_k_lookup",
     "causal_last_k_sources",
     "causal_sum_lookup",
+    "fused_latest1_linear",
     "sort_order",
 ]

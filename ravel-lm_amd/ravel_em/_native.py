@@ -49,6 +49,10 @@ SIGNATURES = {
         _i, [_vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]
     ),
     "ravel_em_gather_rows": (_i, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "ravel_em_latest1_linear_workspace": (_sz, [_i64, _i64, _i64, _i64, _i, _i]),
+    "ravel_em_latest1_linear_fwd": (
+        _i, [_vp, _vp, _i, _vp, _i, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]
+    ),
     "ravel_em_latest_k_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i]),
     "ravel_em_latest_k_bwd": (
         _i, [_vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i, _vp, _vp, _sz, _vp]

@@ -76,3 +76,17 @@ def test_unsupported_payload_dtype_is_a_type_error():
 
     with pytest.raises(TypeError):
         nat.payload_code(torch.int32)
+
+
+def test_fused_latest1_linear_errors_match_reference():
+    # ravel_lm/triton_memory.py:390-395
+    from ravel_em import fused_latest1_linear
+
+    w = torch.zeros(2, 3, 4, dtype=torch.long)
+    p = torch.zeros(2, 3, 4, 8)
+    with pytest.raises(ValueError, match=r"expected write/read \[B,T,C\]"):
+        fused_latest1_linear(w[0], p, None, torch.zeros(5, 32), address_space=9)
+    with pytest.raises(ValueError, match=r"weight must have shape \[M, C \* P\]"):
+        fused_latest1_linear(w, p, None, torch.zeros(5, 31), address_space=9)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fused_latest1_linear(w, p, None, torch.zeros(5, 32), address_space=9)
