@@ -10,13 +10,12 @@
 //   out[n, m] = sum_k A[n, k] * W[m, k],   n = b*T + t, k = c*P + p,
 //   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
 //
-// Tiles: a block computes kRows rows x kCols (= 4 waves x 64) columns over K in
-// chunks of kChunk.  A chunk's A tile is gathered in 16-byte units (8 values;
+// Tiles: a block (8 waves) computes kRows rows x kCols columns over K in chunks
+// of kChunk; wave (g, h) owns rows [64g, 64g+64) and columns [64h, 64h+64).  A chunk's A tile is gathered in 16-byte units (8 values;
 // P % 8 == 0 keeps a unit inside one head), W's tile is read row-major, both
 // go to LDS with rows padded to kLds elements (144 bytes: the 16 rows that one
-// MFMA operand read touches land in distinct banks).  Wave w owns columns
-// [64w, 64w + 64) and all kRows rows: (kRows/16) x 4 tiles of
-// v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to the
+// MFMA operand read touches land in distinct banks).  A wave runs 4 x 4 tiles
+// of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to the
 // payload dtype.  Operand lane layout (checked on the device): A lane l holds
 // row l%16, k (l/16)*8 .. +7; B lane l holds column l%16, the same k; the
 // result lane l holds column l%16, rows (l/16)*4 .. +3.  The epilogue stages
@@ -28,7 +27,9 @@ namespace rem {
 
 namespace {
 
+constexpr int kThreads = 512;  // 8 waves: 2 row groups x 4 column groups of 64 x 64
 constexpr int kRows = 128;
+constexpr int kSrcLds = 32;  // heads whose sources a block stages in LDS
 constexpr int kCols = 256;
 constexpr int kChunk = 64;
 constexpr int kLds = kChunk + 8;
@@ -60,44 +61,54 @@ __device__ __forceinline__ uint16_t round16(float x) {
 }
 
 template <bool F16>
-__global__ __launch_bounds__(256) void gather_gemm_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void gather_gemm_kernel(
     const uint16_t* __restrict__ payload, const int32_t* __restrict__ src,
     const uint16_t* __restrict__ W, int64_t NR, int C, int P, int M, int64_t nsrc,
     uint16_t* __restrict__ out) {
-  constexpr int RT = kRows / 16;  // row tiles per wave
+  constexpr int RT = 4;  // 16-row tiles per wave (64 rows)
   __shared__ __align__(16) uint16_t As[kRows * kLds];
   __shared__ __align__(16) uint16_t Bs[kCols * kLds];
+  __shared__ int32_t Ss[kRows * kSrcLds];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wrow = wave >> 2, wcol = wave & 3;  // 64-row group, 64-column group
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int K = C * P;
+  // The block's sources [kRows][C] (one contiguous run) go to LDS once, so a
+  // chunk's gather costs one memory round trip.
+  const bool src_lds = C <= kSrcLds;
+  if (src_lds) {
+    const int64_t nrow = (NR - row0) < kRows ? (NR - row0) : kRows;
+    for (int i = tid; i < nrow * C; i += kThreads) Ss[i] = src[row0 * C + i];
+    __syncthreads();
+  }
   f32x4_t acc[RT][4];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const bool wave_live = wave * 64 < M;  // columns past M are padding
+  const bool wave_live = wcol * 64 < M;  // columns past M are padding
   // The next chunk's tiles are loaded into registers while the current chunk
   // multiplies out of LDS.
-  constexpr int AU = kRows * 8 / 256;
-  constexpr int BU = kCols * 8 / 256;
+  constexpr int AU = kRows * 8 / kThreads;
+  constexpr int BU = kCols * 8 / kThreads;
   u32x4 av[AU], bv[BU];
   auto load_chunk = [&](int k0) {
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
-      const int u = tid + 256 * q;
+      const int u = tid + kThreads * q;
       const int r = u >> 3, piece = u & 7;
       const int k = k0 + piece * 8;
       const int64_t n = row0 + r;
       av[q] = u32x4{0u, 0u, 0u, 0u};
       if (n < NR && k < K) {
         const int c = k / P;
-        const int32_t s = src[n * C + c];
+        const int32_t s = src_lds ? Ss[r * C + c] : src[n * C + c];
         if (s >= 0 && s < nsrc) av[q] = *(const u32x4*)(payload + (int64_t)s * P + (k - c * P));
       }
     }
 #pragma unroll
     for (int q = 0; q < BU; ++q) {
-      const int u = tid + 256 * q;
+      const int u = tid + kThreads * q;
       const int m = u >> 3, piece = u & 7;
       const int k = k0 + piece * 8;
       bv[q] = (m < M && k < K) ? *(const u32x4*)(W + (int64_t)m * K + k) : u32x4{0u, 0u, 0u, 0u};
@@ -107,12 +118,12 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(
   for (int k0 = 0; k0 < K; k0 += kChunk) {
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
-      const int u = tid + 256 * q;
+      const int u = tid + kThreads * q;
       *(u32x4*)&As[(u >> 3) * kLds + (u & 7) * 8] = av[q];
     }
 #pragma unroll
     for (int q = 0; q < BU; ++q) {
-      const int u = tid + 256 * q;
+      const int u = tid + kThreads * q;
       *(u32x4*)&Bs[(u >> 3) * kLds + (u & 7) * 8] = bv[q];
     }
     __syncthreads();
@@ -124,10 +135,10 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(
         u32x4 b[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          b[j] = *(const u32x4*)&Bs[(wave * 64 + j * 16 + (lane & 15)) * kLds + kk];
+          b[j] = *(const u32x4*)&Bs[(wcol * 64 + j * 16 + (lane & 15)) * kLds + kk];
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
-          const u32x4 a = *(const u32x4*)&As[(i * 16 + (lane & 15)) * kLds + kk];
+          const u32x4 a = *(const u32x4*)&As[(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
         }
@@ -140,23 +151,24 @@ __global__ __launch_bounds__(256) void gather_gemm_kernel(
   uint16_t* Cs = Bs;
   constexpr int CSTRIDE = kCols + 8;
   static_assert(kRows / 2 * CSTRIDE <= kCols * kLds, "epilogue half-tile must fit the B buffer");
+  // Half h holds the rows of row group h.
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    if (wave_live) {
+    if (wave_live && wrow == half) {
 #pragma unroll
-      for (int i = half * RT / 2; i < (half + 1) * RT / 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int r = i * 16 + (lane >> 4) * 4 + e - half * (kRows / 2);
-            const int col = wave * 64 + j * 16 + (lane & 15);
+            const int r = i * 16 + (lane >> 4) * 4 + e;
+            const int col = wcol * 64 + j * 16 + (lane & 15);
             Cs[r * CSTRIDE + col] = round16<F16>(acc[i][j][e]);
           }
     }
     __syncthreads();
     const int upr = M >> 3;  // 16-byte units per output row (M % 8 == 0)
-    for (int u = tid; u < (kRows / 2) * upr; u += 256) {
+    for (int u = tid; u < (kRows / 2) * upr; u += kThreads) {
       const int r = u / upr, piece = u - (u / upr) * upr;
       const int64_t n = row0 + half * (kRows / 2) + r;
       if (n < NR) *(u32x4*)(out + n * M + piece * 8) = *(const u32x4*)&Cs[r * CSTRIDE + piece * 8];
@@ -180,11 +192,11 @@ hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, i
   if (blocks > INT32_MAX || C * P > INT32_MAX) return hipErrorInvalidValue;
   const int64_t nsrc = NR * C;
   if (dtype == kF16)
-    gather_gemm_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(
+    gather_gemm_kernel<true><<<(unsigned)blocks, kThreads, 0, s>>>(
         (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
         (uint16_t*)out);
   else
-    gather_gemm_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(
+    gather_gemm_kernel<false><<<(unsigned)blocks, kThreads, 0, s>>>(
         (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
         (uint16_t*)out);
   return hipGetLastError();
