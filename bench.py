@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--suite", action="store_true",
                     help="time every BASELINE config (cfg1-cfg5), one JSON line per op, instead of the headline")
+    ap.add_argument("--suite-parts", nargs="+", default=None, metavar="PART",
+                    help="with --suite: only these parts (tapes, addresses, decode)")
     return ap.parse_args()
 
 
@@ -88,6 +90,10 @@ def cpu_baseline(w, budget_s):
     }
 
 
+def _wr(addrs, payload):
+    return addrs[0], payload, addrs[1]
+
+
 def suite_cpu_baseline(w, op, budget_s=6.0):
     """The reference CPU path (torch restatement) on one suite workload and op."""
     import torch
@@ -107,6 +113,38 @@ def suite_cpu_baseline(w, op, budget_s=6.0):
         times.sort()
         return times[len(times) // 2], len(times)
 
+    if "_from_" in op:
+        # the reference layer's address ops then its lookup, all on the CPU
+        src = w.source
+        A = w.address_space
+        toks = None if src.n_literal_heads == 0 else src.token_ids.cpu()
+        wl = None if src.write_logits is None else src.write_logits.cpu()
+        rl = None if src.same else src.read_logits.cpu()
+        payload = w.payload.cpu()
+        B, T = payload.shape[:2]
+
+        def addresses():
+            parts_w, parts_r = [], []
+            if toks is not None:
+                lit = torch_ref.literal_addresses(toks, address_space=A, n_heads=src.n_literal_heads,
+                                                  bos_token_id=src.bos_token_id)
+                parts_w.append(lit)
+                parts_r.append(lit)
+            if wl is not None:
+                kw = dict(n_heads=src.n_learned_heads, n_codebooks=src.n_codebooks,
+                          codebook_size=src.codebook_size, address_space=A)
+                parts_w.append(torch_ref.product_codes(wl, **kw))
+                parts_r.append(parts_w[-1] if rl is None else torch_ref.product_codes(rl, **kw))
+            wa = torch.cat(parts_w, dim=-1)
+            return wa, (None if src.same else torch.cat(parts_r, dim=-1))
+
+        if op.startswith("latest_k"):
+            fn = lambda: torch_ref.latest_k(*_wr(addresses(), payload), address_space=A, k=w.k)
+        else:
+            fn = lambda: torch_ref.seg_sum(*_wr(addresses(), payload), address_space=A)
+        med, n = timed(fn, 3)
+        return {"value": B * T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{n} full calls (address ops + lookup), median {med:.4f} s"}
     if op in ("latest_k", "seg_sum"):
         write = w.write.cpu()
         read = None if w.read is None else w.read.cpu()
@@ -163,7 +201,8 @@ def main():
     if args.suite:
         from ravel_em import suite
 
-        suite.run(dev, cpu=None if args.no_cpu_baseline else suite_cpu_baseline)
+        suite.run(dev, cpu=None if args.no_cpu_baseline else suite_cpu_baseline,
+                  parts=tuple(args.suite_parts) if args.suite_parts else suite.PARTS)
         return
     log("generating cfg4 inputs on the device")
     w = workloads.cfg4(dev, adversarial=args.adversarial)

@@ -29,6 +29,7 @@ extern "C" {
 enum {
   RAVEL_EM_INT32 = 1,
   RAVEL_EM_INT64 = 2,
+  RAVEL_EM_ADDR_GEN = 3, /* address code only: addresses produced from a ravel_em_addr_gen */
   RAVEL_EM_FLOAT32 = 10,
   RAVEL_EM_BFLOAT16 = 11,
   RAVEL_EM_FLOAT16 = 12,
@@ -42,6 +43,53 @@ enum {
   RAVEL_EM_EHIP = 2,       /* a HIP launch failed */
   RAVEL_EM_EWORKSPACE = 3  /* workspace smaller than the *_workspace() query */
 };
+
+/*
+ * Produced addresses.  Where an entry point takes `addr_dtype`, the code
+ * RAVEL_EM_ADDR_GEN makes its write_addr / read_addr arguments point to host
+ * descriptors of this type instead of [B,T,C] address tensors: the kernels then
+ * compute the address of record (b, t, c) where they need it (the key build and
+ * the read search) and no address tensor exists.  The descriptor is read during
+ * the call only.  It replaces the address production of the reference's memory
+ * layer, RavelMemoryLayer.forward (ravel_lm/model.py:325-346):
+ *   heads c < n_literal: literal_addresses_from_tokens (ravel_lm/model.py:195-231)
+ *     0  tok,  1  prev1*257 + tok*131 + 17,
+ *     2  prev2*65537 + prev1*257 + tok*131 + 31,
+ *     j  tok*(1009+2j) + t*(9176+j) + j*97   (j >= 3),
+ *     prev1/prev2 = tokens at t-1/t-2 (bos_token_id before the start),
+ *     int64 arithmetic, Python remainder by A;
+ *   heads c >= n_literal: the product codes of ProductCodeAddressor /
+ *     _decode_codes (ravel_lm/model.py:177-187, :303-307): per codebook q the
+ *     argmax (first maximum, NaN counts as the maximum) of codebook_size
+ *     logits, address sum_q code_q * codebook_size^q, remainder by A.
+ * C must equal n_literal + n_learned.  Reads use the read descriptor (NULL =
+ * the write descriptor); in the reference layer the two share the literal
+ * heads and differ in their logits.
+ */
+typedef struct ravel_em_addr_gen {
+  const void* tokens;         /* device [B,T] token ids (needed when n_literal > 0) */
+  int32_t token_dtype;        /* RAVEL_EM_INT32 or RAVEL_EM_INT64 */
+  int32_t n_literal;          /* literal heads */
+  int64_t token_stride_b;     /* element strides of tokens */
+  int64_t token_stride_t;
+  int64_t bos_token_id;
+  const void* logits;         /* device [B,T,n_learned,n_codebooks,codebook_size], last three
+                                 dims contiguous (needed when n_learned > 0) */
+  int32_t logits_dtype;       /* RAVEL_EM_FLOAT32, RAVEL_EM_BFLOAT16 or RAVEL_EM_FLOAT16 */
+  int32_t n_learned;          /* learned (product-code) heads */
+  int32_t n_codebooks;
+  int32_t codebook_size;
+  int64_t logits_stride_b;    /* element strides of logits over b and t */
+  int64_t logits_stride_t;
+} ravel_em_addr_gen;
+
+/*
+ * The addresses of a descriptor as a [B,T,C] tensor (out_dtype RAVEL_EM_INT64
+ * or RAVEL_EM_INT32), in [0, A): torch.cat([literal_addresses_from_tokens(...),
+ * _decode_codes(...)], -1) of ravel_lm/model.py:333-343 in one kernel.
+ */
+int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64_t A,
+                       int out_dtype, void* out, void* stream);
 
 /* Message of the last failed call on this thread ("" when none). */
 const char* ravel_em_last_error(void);
@@ -90,6 +138,9 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
 /*
  * causal_last_k_lookup forward (ravel_lm/ravel_memory.py:52-176).
  *   write_addr, read_addr [B,T,C] int32/int64 (read_addr NULL = write_addr),
+ *   or ravel_em_addr_gen descriptors with RAVEL_EM_ADDR_GEN (as in every entry
+ *   point below that takes addr_dtype, except the decode cache's read, write
+ *   and step),
  *   write_mask [B,T] bool or NULL, payload [B,T,C,D].
  *   out_values [B,T,C,k,D] (payload dtype), out_mask [B,T,C,k] bool,
  *   out_src [B,T,C,k] int32 source record index or -1 (NULL = not wanted).

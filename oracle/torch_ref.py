@@ -123,3 +123,37 @@ def cache_write(values: Tensor, filled: Tensor, addresses: Tensor, payload: Tens
     idx = addresses.long().clamp(0, A - 1)
     values.scatter_(2, idx.view(B, C, 1, 1).expand(B, C, 1, D), payload.unsqueeze(2))
     filled.scatter_(2, idx.view(B, C, 1), torch.ones(B, C, 1, dtype=torch.bool))
+
+
+def literal_addresses(tokens: Tensor, *, address_space: int, n_heads: int, bos_token_id: int) -> Tensor:
+    """literal_addresses_from_tokens, ravel_lm/model.py:195-231: the same torch
+    op sequence (shifted copies padded with bos, int64 products, remainder,
+    stack), for the CPU baseline of the layer's address production."""
+    B, T = tokens.shape
+    toks = tokens.long()
+    A = int(address_space)
+    pad = torch.full((B, 2), int(bos_token_id), dtype=torch.long)
+    prev1 = torch.cat([pad[:, :1], toks[:, :-1]], dim=1)
+    prev2 = torch.cat([pad, toks[:, :-2]], dim=1)
+    heads = []
+    for j in range(n_heads):
+        if j == 0:
+            h = toks
+        elif j == 1:
+            h = prev1 * 257 + toks * 131 + 17
+        elif j == 2:
+            h = prev2 * 65537 + prev1 * 257 + toks * 131 + 31
+        else:
+            pos = torch.arange(T, dtype=torch.long).view(1, T).expand(B, T)
+            h = toks * (1009 + 2 * j) + pos * (9176 + j) + j * 97
+        heads.append(h.remainder(A))
+    return torch.stack(heads, dim=-1)
+
+
+def product_codes(logits: Tensor, *, n_heads: int, n_codebooks: int, codebook_size: int,
+                  address_space: int) -> Tensor:
+    """_decode_codes, ravel_lm/model.py:303-307 (argmax per codebook, codes
+    times powers of codebook_size, summed, remainder)."""
+    codes = logits.reshape(*logits.shape[:-1], n_heads, n_codebooks, codebook_size).argmax(dim=-1)
+    mult = torch.tensor([codebook_size ** q for q in range(n_codebooks)], dtype=torch.long)
+    return (codes.long() * mult).sum(dim=-1).remainder(int(address_space))

@@ -85,8 +85,71 @@ int check_tape(int64_t B, int64_t T, int64_t C, int64_t A) {
   return RAVEL_EM_OK;
 }
 
-int check_addr_dtype(int dt) {
-  if (dt != kI32 && dt != kI64) return fail(RAVEL_EM_EINVAL, "address dtype must be int32 or int64 (code %d)", dt);
+int check_addr_dtype(int dt, bool gen_ok = true) {
+  if (dt == kAddrGen && gen_ok) return RAVEL_EM_OK;
+  if (dt != kI32 && dt != kI64)
+    return fail(RAVEL_EM_EINVAL, "address dtype must be int32 or int64%s (code %d)",
+                gen_ok ? " or RAVEL_EM_ADDR_GEN" : "", dt);
+  return RAVEL_EM_OK;
+}
+
+// Address input of an entry point: the tensor at p, or for RAVEL_EM_ADDR_GEN
+// the host descriptor at p (checked against the C heads of the call).
+int addr_in(const void* p, int dt, int64_t C, AddrIn* out) {
+  out->kind = dt;
+  out->dense = p;
+  if (dt != kAddrGen) return RAVEL_EM_OK;
+  const ravel_em_addr_gen* g = (const ravel_em_addr_gen*)p;
+  if (g->n_literal < 0 || g->n_learned < 0 || (int64_t)g->n_literal + g->n_learned != C)
+    return fail(RAVEL_EM_EINVAL, "address descriptor heads %d literal + %d learned != C=%lld",
+                g->n_literal, g->n_learned, (long long)C);
+  if (g->n_literal > 0) {
+    if (!g->tokens) return fail(RAVEL_EM_EINVAL, "address descriptor: literal heads need tokens");
+    if (g->token_dtype != kI32 && g->token_dtype != kI64)
+      return fail(RAVEL_EM_EINVAL, "token ids must be int32 or int64 (code %d)", g->token_dtype);
+  }
+  if (g->n_learned > 0) {
+    if (!g->logits) return fail(RAVEL_EM_EINVAL, "address descriptor: learned heads need logits");
+    if (g->logits_dtype != kF32 && g->logits_dtype != kBF16 && g->logits_dtype != kF16)
+      return fail(RAVEL_EM_EINVAL, "logits must be float32, bfloat16 or float16 (code %d)",
+                  g->logits_dtype);
+    if (g->n_codebooks < 1 || g->codebook_size < 1)
+      return fail(RAVEL_EM_EINVAL, "n_codebooks and codebook_size must be positive");
+    __int128 span = 1;  // codebook_size ** n_codebooks: the packed code must fit int64
+    for (int q = 0; q < g->n_codebooks && span <= ((__int128)1 << 62); ++q) span *= g->codebook_size;
+    if (span > ((__int128)1 << 62))
+      return fail(RAVEL_EM_EINVAL, "codebook_size ** n_codebooks must be <= 2^62");
+  }
+  AddrGen& a = out->gen;
+  a.tokens = g->tokens;
+  a.tok_dtype = g->token_dtype;
+  a.n_lit = g->n_literal;
+  a.tok_sb = g->token_stride_b;
+  a.tok_st = g->token_stride_t;
+  a.bos = g->bos_token_id;
+  a.logits = g->logits;
+  a.lg_dtype = g->logits_dtype;
+  a.n_learned = g->n_learned;
+  a.ncb = g->n_codebooks;
+  a.cbs = g->codebook_size;
+  a.lg_sb = g->logits_stride_b;
+  a.lg_st = g->logits_stride_t;
+  return RAVEL_EM_OK;
+}
+
+// Write and optional read address inputs of a lookup.
+struct AddrPair {
+  AddrIn w, r;
+  const AddrIn* rp = nullptr;
+};
+
+int addr_pair(const void* waddr, const void* raddr, int dt, int64_t C, AddrPair* out) {
+  if (int rc = addr_in(waddr, dt, C, &out->w)) return rc;
+  out->rp = nullptr;
+  if (raddr) {
+    if (int rc = addr_in(raddr, dt, C, &out->r)) return rc;
+    out->rp = &out->r;
+  }
   return RAVEL_EM_OK;
 }
 
@@ -119,6 +182,33 @@ SortWs<U> take_sort(Bump& bp, const Tape& tp) {
   return w;
 }
 
+// The sort of a call.  Produced write addresses are decoded into the second
+// key buffer, whose only reader, the key build, runs before the first sorting
+// pass overwrites it.
+template <typename U>
+hipError_t sort_call(const AddrIn& wa, const uint8_t* wmask, const Tape& tp, const SortWs<U>& sw,
+                     U** sorted, hipStream_t s, uint32_t* zero = nullptr, int64_t zero_words = 0,
+                     int32_t* link_seg = nullptr) {
+  AddrIn wd;
+  hipError_t e = compact_addresses(wa, tp, sw.kb, &wd, s);
+  if (e != hipSuccess) return e;
+  return sort_tape<U>(wd, wmask, tp, sw.ka, sw.kb, sw.counts, sorted, s, zero, zero_words,
+                      link_seg);
+}
+
+// The read search after the sort (reads = writes when ra is null).  Produced
+// read addresses are decoded into the key buffer that does not hold the sorted
+// keys.
+template <typename U>
+hipError_t read_call(const U* sorted, const AddrIn& wa, const AddrIn* ra, const Tape& tp,
+                     const SortWs<U>& sw, int k, int32_t* src, int32_t* spos, hipStream_t s) {
+  AddrIn rd;
+  void* spare = sorted == sw.ka ? (void*)sw.kb : (void*)sw.ka;
+  hipError_t e = compact_addresses(ra ? *ra : wa, tp, spare, &rd, s);
+  if (e != hipSuccess) return e;
+  return search_reads<U>(sorted, rd, tp, k, src, spos, s);
+}
+
 size_t sort_bytes(const Tape& tp) {
   Bump bp(nullptr);
   if (tp.wide())
@@ -135,11 +225,11 @@ struct LkPlan {
 };
 
 template <typename U>
-int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                  const void* payload, int64_t row_bytes, const Tape& tp, int64_t k,
                  void* out_values, uint8_t* out_mask, int32_t* out_src, void* ws, size_t wsb,
                  hipStream_t s) {
-  const bool link = !raddr && !wmask;
+  const bool link = !ra && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
   // The link writes segment-major sources (src_seg), which one tiled
@@ -149,8 +239,8 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s,
-                              nullptr, 0, link && k == 1 ? src_seg : nullptr);
+  hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
+                              link && k == 1 ? src_seg : nullptr);
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   stage_begin(kStageResolve, s);
@@ -158,7 +248,7 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
     if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
-    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+    e = read_call<U>(sorted, wa, ra, tp, sw, (int)k, src, nullptr, s);
   }
   stage_end(kStageResolve, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
@@ -170,22 +260,22 @@ int latest_k_run(const void* waddr, const void* raddr, bool a64, const uint8_t* 
 }
 
 template <typename U>
-int resolve_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+int resolve_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                 const Tape& tp, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
-  const bool link = !raddr && !wmask;
+  const bool link = !ra && !wmask;
   Bump bp(ws);
   SortWs<U> sw = take_sort<U>(bp, tp);
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, sw.ka, sw.kb, sw.counts, &sorted, s,
-                              nullptr, 0, link && k == 1 ? src_seg : nullptr);
+  hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
+                              link && k == 1 ? src_seg : nullptr);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (link) {
     if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
-    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, (int)k, src, nullptr, s);
+    e = read_call<U>(sorted, wa, ra, tp, sw, (int)k, src, nullptr, s);
   }
   if (e != hipSuccess) return hip_fail(e, "resolve");
   return RAVEL_EM_OK;
@@ -237,17 +327,17 @@ SumWs<U> take_sum(Bump& bp, const Tape& tp, int64_t D, int dtype, bool direct, b
 }
 
 template <typename U>
-int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+int seg_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                 const void* payload, int dtype, const Tape& tp, int64_t D, void* out_sum,
                 uint8_t* out_mask, void* ws, size_t wsb, hipStream_t s) {
-  const bool direct = !raddr && !wmask;
+  const bool direct = !ra && !wmask;
   Bump bp(ws);
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, false);
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s,
-                              (uint32_t*)w.walk, 2 * w.walk_words);
+  hipError_t e = sort_call<U>(wa, wmask, tp, w.sw, &sorted, s, (uint32_t*)w.walk,
+                              2 * w.walk_words);
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (direct) {
@@ -261,7 +351,7 @@ int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
   e = seg_sum<U>(sorted, payload, dtype, tp, D, false, w.S, nullptr, w.tail, w.flag, w.carry,
                  w.walk, s);
   if (e != hipSuccess) return hip_fail(e, "segmented sum");
-  e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
+  e = read_call<U>(sorted, wa, ra, tp, w.sw, 1, nullptr, w.spos, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
   e = gather_rows(w.S, tp.n(), w.spos, tp.n(), D * dtype_size(dtype), out_sum, out_mask, s);
   if (e != hipSuccess) return hip_fail(e, "gather");
@@ -269,19 +359,19 @@ int seg_sum_run(const void* waddr, const void* raddr, bool a64, const uint8_t* w
 }
 
 template <typename U>
-int seg_sum_bwd_run(const void* waddr, const void* raddr, bool a64, const uint8_t* wmask,
+int seg_sum_bwd_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                     const void* grad, int dtype, const Tape& tp, int64_t D, void* grad_payload,
                     void* ws, size_t wsb, hipStream_t s) {
-  const bool direct = !raddr && !wmask;
+  const bool direct = !ra && !wmask;
   Bump bp(ws);
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, true);
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
-  hipError_t e = sort_tape<U>(waddr, a64, wmask, tp, w.sw.ka, w.sw.kb, w.sw.counts, &sorted, s,
-                              (uint32_t*)w.walk, 2 * w.walk_words);
+  hipError_t e = sort_call<U>(wa, wmask, tp, w.sw, &sorted, s, (uint32_t*)w.walk,
+                              2 * w.walk_words);
   if (e != hipSuccess) return hip_fail(e, "sort");
   if (!direct) {
-    e = search_reads<U>(sorted, raddr ? raddr : waddr, a64, tp, 1, nullptr, w.spos, s);
+    e = read_call<U>(sorted, wa, ra, tp, w.sw, 1, nullptr, w.spos, s);
     if (e != hipSuccess) return hip_fail(e, "resolve");
   }
   e = seg_sum_bwd<U>(sorted, w.spos, grad, dtype, tp, D, direct, (float*)w.gacc, w.tail, w.flag,
@@ -303,7 +393,7 @@ void stage_begin(int stage, hipStream_t s) {
   if (!g_prof.on) return;
   const size_t i = g_prof.take();
   if (i == (size_t)-1) return;
-  hipEventRecord(g_prof.pool[i], s);
+  (void)hipEventRecord(g_prof.pool[i], s);
   g_prof.open[stage] = (int)i;
 }
 
@@ -311,7 +401,7 @@ void stage_end(int stage, hipStream_t s) {
   if (!g_prof.on) return;
   const size_t i = g_prof.take();
   if (i == (size_t)-1) return;
-  hipEventRecord(g_prof.pool[i], s);
+  (void)hipEventRecord(g_prof.pool[i], s);
   g_prof.spans.push_back({stage, {(size_t)g_prof.open[stage], i}});
 }
 
@@ -348,7 +438,27 @@ extern "C" {
 
 const char* ravel_em_last_error(void) { return g_err.c_str(); }
 
-int ravel_em_abi_version(void) { return 1; }
+int ravel_em_abi_version(void) { return 2; }
+
+int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64_t A,
+                       int out_dtype, void* out, void* stream) {
+  g_err.clear();
+  if (!gen) return fail(RAVEL_EM_EINVAL, "null pointer");
+  const int64_t C = (int64_t)gen->n_literal + gen->n_learned;
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (out_dtype != kI32 && out_dtype != kI64)
+    return fail(RAVEL_EM_EINVAL, "address output must be int32 or int64 (code %d)", out_dtype);
+  if (out_dtype == kI32 && A > INT32_MAX)
+    return fail(RAVEL_EM_EINVAL, "int32 addresses need address_space <= 2^31-1");
+  AddrIn a;
+  if (int rc = addr_in(gen, kAddrGen, C, &a)) return rc;
+  const Tape tp = make_tape(B, T, C, A, false, kWrap);
+  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (!out) return fail(RAVEL_EM_EINVAL, "null pointer");
+  hipError_t e = write_addresses(a, tp, out_dtype, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "addresses");
+  return RAVEL_EM_OK;
+}
 
 int ravel_em_set_sort_path(int path) {
   g_err.clear();
@@ -412,6 +522,8 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!write_addr || !out_sorted_keys || !out_order) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrIn wa;
+  if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
   hipStream_t s = (hipStream_t)stream;
   const bool keys64 = ravel_em_key_bits(B, T, C, A) == 64;
   auto run = [&](auto tag) -> int {
@@ -421,8 +533,7 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
     int64_t* vprefix = write_mask ? bp.take<int64_t>((size_t)(B * T + 1)) : nullptr;
     if (int rc = check_ws(bp, workspace_bytes)) return rc;
     U* sorted = nullptr;
-    hipError_t e = sort_tape<U>(write_addr, addr_dtype == kI64, write_mask, tp, sw.ka, sw.kb,
-                                sw.counts, &sorted, s);
+    hipError_t e = sort_call<U>(wa, write_mask, tp, sw, &sorted, s);
     if (e != hipSuccess) return hip_fail(e, "sort");
     e = emit_order<U>(sorted, write_mask, vprefix, tp, out_sorted_keys, keys64, out_order, s);
     if (e != hipSuccess) return hip_fail(e, "emit order");
@@ -457,14 +568,15 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!write_addr || !payload || !out_values || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   const int64_t row_bytes = D * dtype_size(payload_dtype);
   hipStream_t s = (hipStream_t)stream;
-  const bool a64 = addr_dtype == kI64;
   if (tp.wide())
-    return latest_k_run<uint64_t>(write_addr, read_addr, a64, write_mask, payload, row_bytes, tp,
-                                  k, out_values, out_mask, out_src, workspace, workspace_bytes, s);
-  return latest_k_run<uint32_t>(write_addr, read_addr, a64, write_mask, payload, row_bytes, tp, k,
-                                out_values, out_mask, out_src, workspace, workspace_bytes, s);
+    return latest_k_run<uint64_t>(ap.w, ap.rp, write_mask, payload, row_bytes, tp, k, out_values,
+                                  out_mask, out_src, workspace, workspace_bytes, s);
+  return latest_k_run<uint32_t>(ap.w, ap.rp, write_mask, payload, row_bytes, tp, k, out_values,
+                                out_mask, out_src, workspace, workspace_bytes, s);
 }
 
 size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
@@ -491,12 +603,13 @@ int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!write_addr || !out_src) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const bool a64 = addr_dtype == kI64;
   if (tp.wide())
-    return resolve_run<uint64_t>(write_addr, read_addr, a64, write_mask, tp, k, out_src, workspace,
+    return resolve_run<uint64_t>(ap.w, ap.rp, write_mask, tp, k, out_src, workspace,
                                  workspace_bytes, s);
-  return resolve_run<uint32_t>(write_addr, read_addr, a64, write_mask, tp, k, out_src, workspace,
+  return resolve_run<uint32_t>(ap.w, ap.rp, write_mask, tp, k, out_src, workspace,
                                workspace_bytes, s);
 }
 
@@ -627,13 +740,14 @@ int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!write_addr || !payload || !out_sum || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const bool a64 = addr_dtype == kI64;
   if (tp.wide())
-    return seg_sum_run<uint64_t>(write_addr, read_addr, a64, write_mask, payload, payload_dtype,
-                                 tp, D, out_sum, out_mask, workspace, workspace_bytes, s);
-  return seg_sum_run<uint32_t>(write_addr, read_addr, a64, write_mask, payload, payload_dtype, tp,
-                               D, out_sum, out_mask, workspace, workspace_bytes, s);
+    return seg_sum_run<uint64_t>(ap.w, ap.rp, write_mask, payload, payload_dtype, tp, D, out_sum,
+                                 out_mask, workspace, workspace_bytes, s);
+  return seg_sum_run<uint32_t>(ap.w, ap.rp, write_mask, payload, payload_dtype, tp, D, out_sum,
+                               out_mask, workspace, workspace_bytes, s);
 }
 
 size_t ravel_em_seg_sum_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
@@ -658,19 +772,19 @@ int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!write_addr || !grad_sum || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const bool a64 = addr_dtype == kI64;
   if (tp.wide())
-    return seg_sum_bwd_run<uint64_t>(write_addr, read_addr, a64, write_mask, grad_sum,
-                                     payload_dtype, tp, D, grad_payload, workspace,
-                                     workspace_bytes, s);
-  return seg_sum_bwd_run<uint32_t>(write_addr, read_addr, a64, write_mask, grad_sum, payload_dtype,
-                                   tp, D, grad_payload, workspace, workspace_bytes, s);
+    return seg_sum_bwd_run<uint64_t>(ap.w, ap.rp, write_mask, grad_sum, payload_dtype, tp, D,
+                                     grad_payload, workspace, workspace_bytes, s);
+  return seg_sum_bwd_run<uint32_t>(ap.w, ap.rp, write_mask, grad_sum, payload_dtype, tp, D,
+                                   grad_payload, workspace, workspace_bytes, s);
 }
 
 static int check_cache(int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,
-                       int64_t k, int64_t D) {
-  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+                       int64_t k, int64_t D, bool gen_ok = false) {
+  if (int rc = check_addr_dtype(addr_dtype, gen_ok)) return rc;
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (B < 0 || C < 0 || A < 1 || k < 1 || D < 1)
     return fail(RAVEL_EM_EINVAL, "bad cache shape B=%lld C=%lld A=%lld k=%lld D=%lld",
@@ -734,10 +848,13 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
                            void* stream) {
   g_err.clear();
   if (int rc = check_tape(B, T, C, A)) return rc;
-  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D, true)) return rc;
   if (B * C == 0) return RAVEL_EM_OK;
   if (!values || !filled || (B * T * C > 0 && (!write_addr || !payload)))
     return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrIn wa;
+  if (B * T * C > 0)
+    if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
   hipStream_t s = (hipStream_t)stream;
   const int64_t row_bytes = D * dtype_size(payload_dtype);
@@ -749,8 +866,7 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
     U* sorted = nullptr;
     hipError_t e = hipSuccess;
     if (tp.n() > 0) {
-      e = sort_tape<U>(write_addr, addr_dtype == kI64, write_mask, tp, sw.ka, sw.kb, sw.counts,
-                       &sorted, s);
+      e = sort_call<U>(wa, write_mask, tp, sw, &sorted, s);
       if (e != hipSuccess) return hip_fail(e, "sort");
     }
     e = cache_prefill<U>(sorted, payload, tp, k, row_bytes, values, filled, s);

@@ -41,6 +41,32 @@ struct Tape {
   bool wide() const { return abits + tbits > 32; }
 };
 
+// Addresses produced inside the kernels from the layer's inputs instead of
+// read from a [B, T, C] tensor: literal heads from token ids, learned heads
+// from product-code logits (the functor GenAddr computes them).  Strides are
+// in elements.
+struct AddrGen {
+  const void* tokens = nullptr;  // [B, T] int32/int64 token ids
+  int tok_dtype = 0;
+  int n_lit = 0;
+  int64_t tok_sb = 0, tok_st = 0;
+  int64_t bos = 0;
+  const void* logits = nullptr;  // [B, T, n_learned, ncb, cbs], last three dims contiguous
+  int lg_dtype = 0;
+  int n_learned = 0, ncb = 0, cbs = 0;
+  int64_t lg_sb = 0, lg_st = 0;
+};
+
+// One address input of a call: a dense [B, T, C] tensor (kind kI32 / kI64,
+// or the compact kU16 / kU32 that the address decode writes) or produced
+// addresses (kind kAddrGen), which the kernels read only after decode_addresses
+// has turned them into a compact dense tensor.
+struct AddrIn {
+  int kind = 0;
+  const void* dense = nullptr;
+  AddrGen gen;
+};
+
 int bit_width_u64(uint64_t x);
 Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);
 
@@ -170,7 +196,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, u
 // its last pass: it then writes the segment-major sources [B,C,T] to link_seg,
 // no sorted keys, and sets *sorted to nullptr.
 template <typename U>
-hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp,
+hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp,
                      U* ka, U* kb, uint32_t* counts, U** sorted, hipStream_t s,
                      uint32_t* zero = nullptr, int64_t zero_words = 0,
                      int32_t* link_seg = nullptr);
@@ -188,8 +214,18 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 template <typename U>
 hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s);
 template <typename U>
-hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const Tape& tp, int k,
-                        int32_t* src, int32_t* spos, hipStream_t s);
+hipError_t search_reads(const U* sorted, const AddrIn& raddr, const Tape& tp, int k, int32_t* src,
+                        int32_t* spos, hipStream_t s);
+// Writes the addresses of `a` as a dense [B, T, C] tensor (int32 or int64 by
+// out_dtype), reduced to [0, A): the materialized form of produced addresses.
+hipError_t write_addresses(const AddrIn& a, const Tape& tp, int out_dtype, void* out,
+                           hipStream_t s);
+// Produced addresses of `a` (kind kAddrGen) decoded into buf as the smallest
+// dense kind that holds [0, A) (kU16, kU32 or kI64; buf holds tp.n() elements
+// of it, at most 8 bytes each, and no more than a sort key buffer's element
+// size); *out describes buf.  Dense inputs pass through unchanged.
+hipError_t compact_addresses(const AddrIn& a, const Tape& tp, void* buf, AddrIn* out,
+                             hipStream_t s);
 
 // out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
@@ -252,7 +288,8 @@ hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s);
 
 // dtype codes shared with the C ABI header.
 enum Dtype : int {
-  kI32 = 1, kI64 = 2,
+  kI32 = 1, kI64 = 2, kAddrGen = 3,
+  kU16 = 4, kU32 = 5,  // compact address kinds, internal only
   kF32 = 10, kBF16 = 11, kF16 = 12, kF64 = 13,
 };
 int dtype_size(int dtype);

@@ -17,6 +17,7 @@
 
 #include <algorithm>
 
+#include "em_addr.h"
 #include "em_common.h"
 
 namespace rem {
@@ -173,9 +174,9 @@ __global__ __launch_bounds__(kLinkThreads) void link1_lds_kernel(const U* __rest
   for (int i = tid; i < nslot; i += kLinkThreads) dst[i] = buf[i];
 }
 
-template <typename U, typename AT>
+template <typename U, typename AS>
 __global__ __launch_bounds__(256) void search_reads_kernel(
-    const U* __restrict__ sorted, const AT* __restrict__ raddr, int64_t N, int64_t T, int64_t C,
+    const U* __restrict__ sorted, const AS raddr, int64_t N, int64_t T, int64_t C,
     int64_t A, int tbits, int trunc32, int k, int32_t* __restrict__ src,
     int32_t* __restrict__ spos) {
   const U tmask = (U)((((uint64_t)1) << tbits) - 1);
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(256) void search_reads_kernel(
     const int64_t rem_ = r - b * TC;
     const int64_t t = rem_ / C;
     const int64_t c = rem_ - t * C;
-    const int64_t a = reduce_addr((int64_t)raddr[r], A, kWrap, trunc32 != 0);
+    const int64_t a = reduce_addr(raddr(b, t, c), A, kWrap, trunc32 != 0);
     const int64_t segbase = (b * C + c) * T;
     const U* s = sorted + segbase;
     const U target = ((U)a << tbits) | (U)t;
@@ -236,9 +237,9 @@ constexpr int kSearchLdsBytes = 64 * 1024;
 constexpr int kSearchTile = 2048;
 constexpr int kSearchIlp = 4;
 
-template <typename U, typename AT>
+template <typename U, typename AS>
 __global__ __launch_bounds__(256) void search_lds_kernel(
-    const U* __restrict__ sorted, const AT* __restrict__ raddr, int64_t T, int64_t C, int64_t A,
+    const U* __restrict__ sorted, const AS raddr, int64_t T, int64_t C, int64_t A,
     int tbits, int trunc32, int k, int top, int64_t ntile, int64_t nseg,
     int32_t* __restrict__ src, int32_t* __restrict__ spos) {
   extern __shared__ __align__(16) unsigned char search_lds[];
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(256) void search_lds_kernel(
     for (int m = 0; m < kSearchIlp; ++m) {
       const int tl = base + m * 256 + (int)threadIdx.x;
       const int t = t0 + (tl < nt ? tl : 0);
-      a[m] = reduce_addr((int64_t)raddr[(b * T + t) * C + c], A, kWrap, trunc32 != 0);
+      a[m] = reduce_addr(raddr(b, t, c), A, kWrap, trunc32 != 0);
       target[m] = ((U)a[m] << tbits) | (U)t;
       lo[m] = 0;
     }
@@ -542,8 +543,8 @@ hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src, hipSt
 }
 
 template <typename U>
-hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const Tape& tp, int k,
-                        int32_t* src, int32_t* spos, hipStream_t s) {
+hipError_t search_reads(const U* sorted, const AddrIn& raddr, const Tape& tp, int k, int32_t* src,
+                        int32_t* spos, hipStream_t s) {
   const int64_t N = tp.n();
   if (N == 0) return hipSuccess;
   const size_t lds = (size_t)(tp.T + tp.T / 64 + 1) * sizeof(U);  // padded: word p + p/64
@@ -552,26 +553,19 @@ hipError_t search_reads(const U* sorted, const void* raddr, bool addr64, const T
     while ((int64_t)top * 2 <= tp.T) top *= 2;  // highest power of two <= T
     const int64_t ntile = (tp.T + kSearchTile - 1) / kSearchTile;
     const unsigned g = xcd_grid(tp.nseg() * ntile, 1, (int64_t)1 << 31);
-    if (addr64)
-      search_lds_kernel<U, int64_t><<<g, 256, lds, s>>>(sorted, (const int64_t*)raddr, tp.T, tp.C,
-                                                        tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k,
-                                                        top, ntile, tp.nseg(), src, spos);
-    else
-      search_lds_kernel<U, int32_t><<<g, 256, lds, s>>>(sorted, (const int32_t*)raddr, tp.T, tp.C,
-                                                        tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k,
-                                                        top, ntile, tp.nseg(), src, spos);
-    return hipGetLastError();
+    return with_addr(raddr, tp, [&](auto ra) {
+      search_lds_kernel<U, decltype(ra)><<<g, 256, lds, s>>>(
+          sorted, ra, tp.T, tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k, top, ntile, tp.nseg(),
+          src, spos);
+      return hipGetLastError();
+    });
   }
   const unsigned grid = grid_for(N, 256);
-  if (addr64)
-    search_reads_kernel<U, int64_t><<<grid, 256, 0, s>>>(sorted, (const int64_t*)raddr, N, tp.T,
-                                                         tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0,
-                                                         k, src, spos);
-  else
-    search_reads_kernel<U, int32_t><<<grid, 256, 0, s>>>(sorted, (const int32_t*)raddr, N, tp.T,
-                                                         tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0,
-                                                         k, src, spos);
-  return hipGetLastError();
+  return with_addr(raddr, tp, [&](auto ra) {
+    search_reads_kernel<U, decltype(ra)><<<grid, 256, 0, s>>>(
+        sorted, ra, N, tp.T, tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k, src, spos);
+    return hipGetLastError();
+  });
 }
 
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
@@ -624,9 +618,9 @@ hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64
 
 template hipError_t link_same<uint32_t>(const uint32_t*, const Tape&, int, int32_t*, hipStream_t);
 template hipError_t link_same<uint64_t>(const uint64_t*, const Tape&, int, int32_t*, hipStream_t);
-template hipError_t search_reads<uint32_t>(const uint32_t*, const void*, bool, const Tape&, int,
+template hipError_t search_reads<uint32_t>(const uint32_t*, const AddrIn&, const Tape&, int,
                                            int32_t*, int32_t*, hipStream_t);
-template hipError_t search_reads<uint64_t>(const uint64_t*, const void*, bool, const Tape&, int,
+template hipError_t search_reads<uint64_t>(const uint64_t*, const AddrIn&, const Tape&, int,
                                            int32_t*, int32_t*, hipStream_t);
 
 }  // namespace rem

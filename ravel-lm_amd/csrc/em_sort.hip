@@ -14,6 +14,7 @@
 // Only the address bits are sorted: the time bits are already ascending in
 // the input, and LSD passes are stable, so the result is ordered by (a, t).
 
+#include "em_addr.h"
 #include "em_common.h"
 
 namespace rem {
@@ -26,9 +27,9 @@ constexpr int kTile = kSortThreads * kSortItems;  // keys per tile
 constexpr int kRadix = 256;
 constexpr int kPackTT = 64;  // time steps per pack block (upper bound)
 
-template <typename U, typename AT>
+template <typename U, typename AS>
 __global__ __launch_bounds__(256) void pack_keys_kernel(
-    const AT* __restrict__ addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
+    const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int tt_max, U* __restrict__ keys) {
   extern __shared__ unsigned char smem_raw[];
   U* tile = reinterpret_cast<U*>(smem_raw);  // [C][tt_max + 1]
@@ -39,11 +40,10 @@ __global__ __launch_bounds__(256) void pack_keys_kernel(
   const int Ci = (int)C;
   const int n = tt * Ci;
   const int pitch = tt_max + 1;
-  const int64_t base = (b * T + t0) * C;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int tl = i / Ci;
     const int c = i - tl * Ci;
-    int64_t a = reduce_addr((int64_t)addr[base + i], A, mode, trunc32 != 0);
+    int64_t a = reduce_addr(addr(b, t0 + tl, c), A, mode, trunc32 != 0);
     if (wmask && !wmask[b * T + t0 + tl]) a = A;  // masked: sentinel sorts last
     tile[c * pitch + tl] = ((U)a << tbits) | (U)(t0 + tl);
   }
@@ -270,9 +270,9 @@ __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t wor
 // with per-(segment, tile) histograms of every digit pass.  Sibling head
 // groups of one time tile are consecutive logical blocks, which xcd_block
 // places on one XCD, so the 128-byte address rows they share stay in one L2.
-template <typename U, typename AT>
+template <typename U, typename AS>
 __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
-    const AT* __restrict__ addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
+    const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int npass, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
     uint32_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
@@ -295,14 +295,13 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
   const int hw = cc * per;
   for (int i = threadIdx.x; i < hw; i += kPackThreads) h[i] = 0;
   __syncthreads();
-  const AT* arow = addr + (b * T + t0) * C + c0;
   for (int i0 = 0; i0 < n; i0 += kPackThreads * kPackBatch) {
-    AT av[kPackBatch];
+    int64_t av[kPackBatch];
 #pragma unroll
     for (int j = 0; j < kPackBatch; ++j) {  // all loads first: one memory latency per batch
       const int i = i0 + j * kPackThreads + threadIdx.x;
       const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)cc);
-      av[j] = i < n ? arow[(int64_t)tl * C + (i - tl * cc)] : AT(0);
+      av[j] = i < n ? addr(b, t0 + tl, c0 + (i - tl * cc)) : 0;
     }
 #pragma unroll
     for (int j = 0; j < kPackBatch; ++j) {
@@ -310,7 +309,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
       if (i < n) {
         const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)cc);
         const int cl = i - tl * cc;
-        int64_t a = reduce_addr((int64_t)av[j], A, mode, trunc32 != 0);
+        int64_t a = reduce_addr(av[j], A, mode, trunc32 != 0);
         if (wmask && !wmask[b * T + t0 + tl]) a = A;
         const U u = ((U)a << tbits) | (U)(t0 + tl);
         tile[cl * pitch + tl] = u;
@@ -821,7 +820,7 @@ size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
 }
 
 template <typename U>
-static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* wmask,
+static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
                                   const Tape& tp, PackPlan pl, U* ka, U* kb, uint32_t* words,
                                   U** sorted, hipStream_t s, uint32_t* zero, int64_t zero_words,
                                   int32_t* link_seg) {
@@ -848,14 +847,13 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   // Divisors of the pack index math (the last head group / time tile of a row
   // may be smaller and then divides the slow way).
   const FastDiv by_cc = make_fastdiv((uint32_t)pl.CC), by_tt = make_fastdiv((uint32_t)tt);
-  if (addr64)
-    pack_hist_kernel<U, int64_t><<<pgrid, kPackThreads, 0, s>>>(
-        (const int64_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
-  else
-    pack_hist_kernel<U, int32_t><<<pgrid, kPackThreads, 0, s>>>(
-        (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt,
-        pl.CC, ncg, npass, nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
+  hipError_t e = with_addr(addr, tp, [&](auto src) {
+    pack_hist_kernel<U, decltype(src)><<<pgrid, kPackThreads, 0, s>>>(
+        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, npass,
+        nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
+    return hipGetLastError();
+  });
+  if (e != hipSuccess) return e;
   // Pass-0 tile offsets and the digit bases of every pass, from the pack
   // histograms: one block per (segment, pass) for short segments, else one
   // 1024-thread block per segment.
@@ -872,7 +870,7 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
   uint32_t* next0 = npass > 1 ? status[0] : nullptr;
   scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
       ka, kb, offs, binbase, npass, tp.T, nsct, nblk0, tp.tbits, next0, status_words);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   U* cur = kb;
   U* alt = ka;
@@ -907,13 +905,13 @@ static hipError_t sort_tape_fused(const void* addr, bool addr64, const uint8_t* 
 }
 
 template <typename U>
-hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const Tape& tp, U* ka,
+hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, U* ka,
                      U* kb, uint32_t* counts, U** sorted, hipStream_t s, uint32_t* zero,
                      int64_t zero_words, int32_t* link_seg) {
   if (tp.fused) {
     const PackPlan pl = fused_plan(tp, sizeof(U));
     if (pl.TT)
-      return sort_tape_fused<U>(addr, addr64, wmask, tp, pl, ka, kb, counts, sorted, s, zero,
+      return sort_tape_fused<U>(addr, wmask, tp, pl, ka, kb, counts, sorted, s, zero,
                                 zero_words, link_seg);
   }
   if (zero && zero_words > 0) {
@@ -924,13 +922,11 @@ hipError_t sort_tape(const void* addr, bool addr64, const uint8_t* wmask, const 
   const size_t shm = (size_t)tp.C * (tt + 1) * sizeof(U);
   const int64_t ntb = (tp.T + tt - 1) / tt;
   const unsigned grid = (unsigned)(tp.B * ntb);
-  if (addr64)
-    pack_keys_kernel<U, int64_t><<<grid, 256, shm, s>>>(
-        (const int64_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, ka);
-  else
-    pack_keys_kernel<U, int32_t><<<grid, 256, shm, s>>>(
-        (const int32_t*)addr, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, ka);
-  hipError_t e = hipGetLastError();
+  hipError_t e = with_addr(addr, tp, [&](auto src) {
+    pack_keys_kernel<U, decltype(src)><<<grid, 256, shm, s>>>(
+        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, ka);
+    return hipGetLastError();
+  });
   if (e != hipSuccess) return e;
   const int ntiles = (int)((tp.T + kTile - 1) / kTile);
   const int64_t nblocks = tp.nseg() * ntiles;
@@ -973,10 +969,10 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
   return hipGetLastError();
 }
 
-template hipError_t sort_tape<uint32_t>(const void*, bool, const uint8_t*, const Tape&, uint32_t*,
+template hipError_t sort_tape<uint32_t>(const AddrIn&, const uint8_t*, const Tape&, uint32_t*,
                                         uint32_t*, uint32_t*, uint32_t**, hipStream_t, uint32_t*,
                                         int64_t, int32_t*);
-template hipError_t sort_tape<uint64_t>(const void*, bool, const uint8_t*, const Tape&, uint64_t*,
+template hipError_t sort_tape<uint64_t>(const AddrIn&, const uint8_t*, const Tape&, uint64_t*,
                                         uint64_t*, uint32_t*, uint64_t**, hipStream_t, uint32_t*,
                                         int64_t, int32_t*);
 template hipError_t emit_order<uint32_t>(const uint32_t*, const uint8_t*, int64_t*, const Tape&,

@@ -4,8 +4,11 @@ Drop-in for the reference module ``ravel_lm/ravel_memory.py``: the public
 functions below keep its names and signatures and run as hand-written HIP
 kernels for gfx950 behind the C ABI in include/ravel_em.h.  ``fused_latest1_linear``
 replaces the reference's fused arm ``triton_fused_latest1_linear``
-(ravel_lm/triton_memory.py:477-485).
+(ravel_lm/triton_memory.py:477-485).  ``LayerAddresses`` lets the lookups
+produce the memory layer's addresses (ravel_lm/model.py:195-231, :303-307)
+inside their kernels.
 """
+from .addressing import LayerAddresses, literal_addresses_from_tokens, product_code_addresses
 from .fused import fused_latest1_linear
 from .ravel_memory import (
     RavelLayerCache,
@@ -17,11 +20,14 @@ from .ravel_memory import (
 )
 
 __all__ = [
+    "LayerAddresses",
     "RavelLayerCache",
     "_composite_key_dtype",
     "causal_last_k_lookup",
     "causal_last_k_sources",
     "causal_sum_lookup",
     "fused_latest1_linear",
+    "literal_addresses_from_tokens",
+    "product_code_addresses",
     "sort_order",
 ]

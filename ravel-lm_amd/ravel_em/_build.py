@@ -16,7 +16,7 @@ CSRC = os.path.join(PKG_ROOT, "csrc")
 OBJ_DIR = os.path.join(PKG_ROOT, "_build")
 SOURCES = [
     "em_api.hip", "em_sort.hip", "em_lookup.hip", "em_sum.hip", "em_cache.hip", "em_backward.hip",
-    "em_fuse.hip",
+    "em_fuse.hip", "em_addr.hip",
 ]
 ARCH = os.environ.get("RAVEL_EM_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

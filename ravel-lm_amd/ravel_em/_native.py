@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 # dtype codes (include/ravel_em.h)
 INT32, INT64 = 1, 2
+ADDR_GEN = 3  # address code: write/read pointers are AddrGen descriptors
 FLOAT32, BFLOAT16, FLOAT16, FLOAT64 = 10, 11, 12, 13
 
 _PAYLOAD_CODES = {
@@ -28,11 +29,25 @@ _PAYLOAD_CODES = {
 _ADDR_CODES = {torch.int32: INT32, torch.int64: INT64}
 
 _vp, _i, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+_i32 = ctypes.c_int32
+
+
+class AddrGen(ctypes.Structure):
+    """struct ravel_em_addr_gen of include/ravel_em.h (field order and types)."""
+
+    _fields_ = [
+        ("tokens", _vp), ("token_dtype", _i32), ("n_literal", _i32),
+        ("token_stride_b", _i64), ("token_stride_t", _i64), ("bos_token_id", _i64),
+        ("logits", _vp), ("logits_dtype", _i32), ("n_learned", _i32),
+        ("n_codebooks", _i32), ("codebook_size", _i32),
+        ("logits_stride_b", _i64), ("logits_stride_t", _i64),
+    ]
 
 # name -> (restype, argtypes); must list every function of include/ravel_em.h
 SIGNATURES = {
     "ravel_em_last_error": (ctypes.c_char_p, []),
     "ravel_em_abi_version": (_i, []),
+    "ravel_em_addresses": (_i, [_vp, _i64, _i64, _i64, _i, _vp, _vp]),
     "ravel_em_key_bits": (_i, [_i64, _i64, _i64, _i64]),
     "ravel_em_set_sort_path": (_i, [_i]),
     "ravel_em_profile_start": (_i, []),
@@ -125,6 +140,34 @@ def payload_code(dtype: torch.dtype) -> int:
 
 def addr_code(dtype: torch.dtype) -> int:
     return _ADDR_CODES[dtype]
+
+
+def addr_gen(tokens: Optional[torch.Tensor], n_literal: int, bos_token_id: int,
+             logits: Optional[torch.Tensor], n_learned: int, n_codebooks: int,
+             codebook_size: int) -> AddrGen:
+    """Descriptor of produced addresses.  tokens is [B, T] int32/int64, logits
+    [B, T, n_learned * n_codebooks * codebook_size] with a unit last stride;
+    both are read by the kernels through their strides."""
+    g = AddrGen()
+    if n_literal > 0:
+        g.tokens = tokens.data_ptr()
+        g.token_dtype = _ADDR_CODES[tokens.dtype]
+        g.token_stride_b, g.token_stride_t = tokens.stride(0), tokens.stride(1)
+    g.n_literal = n_literal
+    g.bos_token_id = bos_token_id
+    if n_learned > 0:
+        g.logits = logits.data_ptr()
+        g.logits_dtype = _PAYLOAD_CODES[logits.dtype]
+        g.logits_stride_b, g.logits_stride_t = logits.stride(0), logits.stride(1)
+    g.n_learned = n_learned
+    g.n_codebooks = n_codebooks
+    g.codebook_size = codebook_size
+    return g
+
+
+def ref(desc: Optional[AddrGen]) -> Optional[int]:
+    """Address of a descriptor for a void* argument (None stays NULL)."""
+    return None if desc is None else ctypes.addressof(desc)
 
 
 def require_device(*tensors: Optional[torch.Tensor]) -> None:

@@ -22,6 +22,7 @@ import torch
 
 from . import _native as nat
 from . import _ops
+from .addressing import LayerAddresses
 
 Tensor = torch.Tensor
 
@@ -73,7 +74,7 @@ def _setup(ctx, inputs, output):
     ctx.mark_non_differentiable(src)
 
 
-def _backward(ctx, grad_out, _grad_src):
+def _grads(ctx, grad_out, need_payload: bool, need_weight: bool):
     """ravel_lm/triton_memory.py:428-475: grad_weight = grad^T @ read_flat,
     grad_payload = scatter of grad @ weight through the sources."""
     src, payloads, weight = ctx.saved_tensors
@@ -81,16 +82,75 @@ def _backward(ctx, grad_out, _grad_src):
     M = weight.shape[0]
     grad2d = grad_out.reshape(B * T, M).to(payloads.dtype)
     grad_weight = grad_payload = None
-    if ctx.needs_input_grad[3]:
+    if need_weight:
         read_flat = gather_read_rows(payloads, src)
         grad_weight = torch.matmul(grad2d.t(), read_flat.reshape(B * T, C * P)).to(weight.dtype)
-    if ctx.needs_input_grad[1]:
+    if need_payload:
         grad_read = torch.matmul(grad2d, weight).reshape(B, T, C, 1, P).contiguous()
         grad_payload = _ops.latest_k_backward(src.view(B, T, C, 1), grad_read, ctx.chain)
-    return None, grad_payload, None, grad_weight, None
+    return grad_payload, grad_weight
+
+
+def _backward(ctx, grad_out, _grad_src):
+    gp, gw = _grads(ctx, grad_out, ctx.needs_input_grad[1], ctx.needs_input_grad[3])
+    return None, gp, None, gw, None
 
 
 _latest1_linear.register_autograd(_backward, setup_context=_setup)
+
+
+@torch.library.custom_op("ravel_em::latest1_linear_gen", mutates_args=())
+def _latest1_linear_gen(tokens: Optional[Tensor], write_logits: Optional[Tensor],
+                        read_logits: Optional[Tensor], payloads: Tensor, weight: Tensor,
+                        n_literal: int, bos: int, n_learned: int, ncb: int, cbs: int,
+                        address_space: int) -> Tuple[Tensor, Tensor]:
+    B, T, C, P = payloads.shape
+    M = weight.shape[0]
+    dev = payloads.device
+    w = nat.addr_gen(tokens, n_literal, bos, write_logits, n_learned, ncb, cbs)
+    r = None if read_logits is None else nat.addr_gen(tokens, n_literal, bos, read_logits,
+                                                      n_learned, ncb, cbs)
+    if _mfma_ok(payloads, weight):
+        lib = nat.library()
+        src = torch.empty(B, T, C, dtype=torch.int32, device=dev)
+        out = payloads.new_empty(B, T, M)
+        nbytes = lib.ravel_em_latest1_linear_workspace(B, T, C, address_space, int(r is not None), 1)
+        ws = nat.workspace(nbytes, dev)
+        nat.check(lib.ravel_em_latest1_linear_fwd(
+            nat.ref(w), nat.ref(r), nat.ADDR_GEN, nat.ptr(payloads), nat.payload_code(payloads.dtype),
+            nat.ptr(weight), B, T, C, P, M, address_space, nat.ptr(out), nat.ptr(src), nat.ptr(ws),
+            ws.numel(), nat.stream_of(payloads)))
+        return out, src
+    from .addressing import latest_k_gen
+
+    values, _, s = latest_k_gen(tokens, write_logits, read_logits, payloads, None, n_literal, bos,
+                                n_learned, ncb, cbs, address_space, 1, True)
+    out = torch.matmul(values.reshape(B * T, C * P), weight.t()).reshape(B, T, M)
+    return out, s.view(B, T, C)
+
+
+@_latest1_linear_gen.register_fake
+def _latest1_linear_gen_fake(tokens, write_logits, read_logits, payloads, weight, n_literal, bos,
+                             n_learned, ncb, cbs, address_space):
+    B, T, C, P = payloads.shape
+    return (payloads.new_empty(B, T, weight.shape[0]),
+            torch.empty(B, T, C, dtype=torch.int32, device=payloads.device))
+
+
+def _setup_gen(ctx, inputs, output):
+    payloads, weight = inputs[3], inputs[4]
+    _, src = output
+    ctx.save_for_backward(src, payloads, weight)
+    ctx.chain = inputs[2] is None
+    ctx.mark_non_differentiable(src)
+
+
+def _backward_gen(ctx, grad_out, _grad_src):
+    gp, gw = _grads(ctx, grad_out, ctx.needs_input_grad[3], ctx.needs_input_grad[4])
+    return (None, None, None, gp, gw) + (None,) * 6
+
+
+_latest1_linear_gen.register_autograd(_backward_gen, setup_context=_setup_gen)
 
 
 def gather_read_rows(payloads: Tensor, src: Tensor) -> Tensor:
@@ -117,7 +177,11 @@ def fused_latest1_linear(
     Same contract as the reference's ``triton_fused_latest1_linear``
     (ravel_lm/triton_memory.py:390-395): write/read addresses [B,T,C], payloads
     [B,T,C,P], weight [M, C*P]; ``read_addresses=None`` reads where it writes.
+    ``write_addresses`` may be a LayerAddresses (then read_addresses is None):
+    the addresses are produced inside the sort and the read search.
     """
+    if isinstance(write_addresses, LayerAddresses):
+        return _fused_gen(write_addresses, payloads, read_addresses, weight, address_space)
     if payloads.ndim != 4 or write_addresses.ndim != 3 or (
         read_addresses is not None and read_addresses.ndim != 3
     ):
@@ -139,4 +203,26 @@ def fused_latest1_linear(
     w, r = _prepare(write_addresses, read_addresses, key_dtype)
     out, _ = _latest1_linear(w, payloads.contiguous(), r, weight.to(payloads.dtype).contiguous(),
                              int(address_space))
+    return out
+
+
+def _fused_gen(src: LayerAddresses, payloads: Tensor, read_addresses, weight: Tensor,
+               address_space: int) -> Tensor:
+    if read_addresses is not None:
+        raise ValueError("with LayerAddresses the read addresses come from its read_logits; "
+                         "read_addresses must be None")
+    B, T = src._check()
+    if payloads.ndim != 4 or payloads.shape[:3] != (B, T, src.heads):
+        raise ValueError("expected payloads [B,T,C,P] with C = literal + learned heads")
+    C, P = src.heads, payloads.shape[-1]
+    M = weight.shape[0]
+    if weight.ndim != 2 or weight.shape != (M, C * P):
+        raise ValueError("weight must have shape [M, C * P]")
+    if address_space <= 0:
+        raise ValueError("address_space must be positive")
+    tok, wl, rl = src.tensors()
+    nat.require_device(payloads, weight, tok, wl, rl)
+    out, _ = _latest1_linear_gen(tok, wl, rl, payloads.contiguous(),
+                                 weight.to(payloads.dtype).contiguous(), *src.cfg(),
+                                 int(address_space))
     return out

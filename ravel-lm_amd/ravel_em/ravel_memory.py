@@ -20,6 +20,7 @@ import torch
 
 from . import _native as nat
 from . import _ops
+from .addressing import LayerAddresses, last_k_lookup, sum_lookup
 
 Tensor = torch.Tensor
 
@@ -57,6 +58,12 @@ def _prepare(write_addresses: Tensor, read_addresses: Optional[Tensor], key_dtyp
     return w, r
 
 
+def _no_read(read_addresses) -> None:
+    if read_addresses is not None:
+        raise ValueError("with LayerAddresses the read addresses come from its read_logits; "
+                         "read_addresses must be None")
+
+
 def causal_last_k_lookup(
     write_addresses: Tensor,
     payloads: Tensor,
@@ -73,7 +80,9 @@ def causal_last_k_lookup(
     ``(j+1)``-th most recent.  Reference: ravel_lm/ravel_memory.py:52-176.
 
     Args:
-        write_addresses: [B, T, C] integer addresses for writes.
+        write_addresses: [B, T, C] integer addresses for writes, or a
+                         LayerAddresses whose write and read addresses the
+                         kernels produce (then read_addresses must be None).
         payloads:        [B, T, C, D] payload tensor.
         read_addresses:  [B, T, C] integer read addresses. Defaults to writes.
         address_space:   number of legal addresses per memory head (addresses
@@ -85,6 +94,11 @@ def causal_last_k_lookup(
         values: [B, T, C, k, D] (missing slots are zero)
         mask:   [B, T, C, k] true where a causal record existed.
     """
+    if isinstance(write_addresses, LayerAddresses):
+        _no_read(read_addresses)
+        values, mask, _ = last_k_lookup(write_addresses, payloads, address_space=address_space,
+                                        k=k, write_mask=write_mask)
+        return values, mask
     same = read_addresses is None or read_addresses is write_addresses
     if read_addresses is None:
         read_addresses = write_addresses
@@ -125,8 +139,13 @@ def causal_last_k_sources(
     index ``(b*T + t_src)*C + c`` of the record each slot was copied from, or -1.
     The reference's MPS and Triton arms expose the same source index
     (ravel_lm/mps_memory.py:109-141, triton_latest1.py:60-63), which
-    experiments/chime_arm.py:53-70 consumes.
+    experiments/chime_arm.py:53-70 consumes.  ``write_addresses`` may be a
+    LayerAddresses, as in causal_last_k_lookup.
     """
+    if isinstance(write_addresses, LayerAddresses):
+        _no_read(read_addresses)
+        return last_k_lookup(write_addresses, payloads, address_space=address_space, k=k,
+                             write_mask=write_mask, want_src=True)
     if read_addresses is None:
         read_addresses = write_addresses
     same = read_addresses is write_addresses
@@ -160,8 +179,13 @@ def causal_sum_lookup(
     ``(batch, head, address)`` and time ``< t``, and whether any existed.
     Reference: ravel_lm/ravel_memory.py:179-241.  Sums accumulate in fp32 for
     16-bit payloads and fp64 for 32/64-bit payloads, rounded once to the payload
-    dtype.
+    dtype.  ``write_addresses`` may be a LayerAddresses, as in
+    causal_last_k_lookup.
     """
+    if isinstance(write_addresses, LayerAddresses):
+        _no_read(read_addresses)
+        return sum_lookup(write_addresses, payloads, address_space=address_space,
+                          write_mask=write_mask)
     same = read_addresses is None or read_addresses is write_addresses
     if read_addresses is None:
         read_addresses = write_addresses

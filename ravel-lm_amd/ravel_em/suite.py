@@ -7,6 +7,11 @@ line per measurement:
   seg_sum    causal_sum_lookup on the same tape
   prefill    RavelLayerCache.prefill of the cfg5 decode cache
   decode     cfg5 RavelLayerCache.step, eager and replayed from a HIP graph
+  *_from_*   the memory layer's address production and lookup together
+             (cfg1/cfg2 literal heads from token ids, cfg3 product codes from
+             bf16 logits): the reference's torch address ops then the lookup
+             ("chain"), the address kernel then the lookup ("kernel"), and
+             the lookup producing its addresses in place ("fused")
 
 Each op is timed with HIP events around every call on torch's current stream
 (warmup first, then the median of the calls).  Bytes are the algorithmic bytes
@@ -76,6 +81,81 @@ def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None
     return lines
 
 
+def reference_addresses(src, A: int):
+    """The reference layer's address ops on the device (ravel_lm/model.py:195-231,
+    :303-307, :338-346): torch elementwise ops, argmax, cat."""
+    parts_w, parts_r = [], []
+    if src.n_literal_heads > 0:
+        lit = workloads.literal_addresses(src.token_ids, address_space=A, n_heads=src.n_literal_heads,
+                                          bos=src.bos_token_id)
+        parts_w.append(lit)
+        parts_r.append(lit)
+    if src.n_learned_heads > 0:
+        H, Q, S = src.n_learned_heads, src.n_codebooks, src.codebook_size
+        mult = torch.tensor([S ** q for q in range(Q)], device=src.write_logits.device)
+
+        def dec(lg):
+            codes = lg.reshape(*lg.shape[:-1], H, Q, S).argmax(dim=-1).long()
+            return (codes * mult).sum(dim=-1).remainder(A)
+
+        parts_w.append(dec(src.write_logits))
+        parts_r.append(dec(src.read_logits) if src.read_logits is not None else parts_w[-1])
+    w = torch.cat(parts_w, dim=-1)
+    r = w if src.same else torch.cat(parts_r, dim=-1)
+    return w, r
+
+
+def address_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None,
+                  with_sum: bool = False) -> List[dict]:
+    """latest-k (and optionally the sum) of a workload whose addresses come from
+    its layer inputs, in the three forms chain / kernel / fused."""
+    B, T, C, D = w.shape
+    src, A, k = w.source, w.address_space, w.k
+    inp = f"from_{'logits' if src.n_learned_heads else 'tokens'}"
+    in_bytes = 0
+    if src.n_literal_heads:
+        in_bytes += src.token_ids.numel() * src.token_ids.element_size()
+    for lg in (src.write_logits, src.read_logits if not src.same else None):
+        if lg is not None:
+            in_bytes += lg.numel() * lg.element_size()
+    esz = w.payload.element_size()
+    N = B * T * C
+
+    def lookup(wa, ra):
+        return causal_last_k_lookup(wa, w.payload, ra, address_space=A, k=k)
+
+    forms = {
+        "chain": lambda: lookup(*reference_addresses(src, A)),
+        "kernel": lambda: lookup(*src.materialize(address_space=A)),
+        "fused": lambda: causal_last_k_lookup(src, w.payload, address_space=A, k=k),
+    }
+    lk_bytes = in_bytes + N * D * esz + N * k * D * esz + N * k
+    lines = []
+    for form, fn in forms.items():
+        us = statistics.median(time_calls(fn, iters=iters))
+        lines.append(_line(w.name, f"latest_k_{inp}_{form}", us, lk_bytes, B * T, shape=[B, T, C, D],
+                           k=k, A=A, heads={"literal": src.n_literal_heads, "learned": src.n_learned_heads}))
+    if with_sum:
+        sforms = {
+            "chain": lambda: _sum_chain(reference_addresses(src, A), w.payload, A),
+            "fused": lambda: causal_sum_lookup(src, w.payload, address_space=A),
+        }
+        sum_bytes = in_bytes + N * D * esz + N * D * esz + N
+        for form, fn in sforms.items():
+            us = statistics.median(time_calls(fn, iters=iters))
+            lines.append(_line(w.name, f"seg_sum_{inp}_{form}", us, sum_bytes, B * T, shape=[B, T, C, D], A=A))
+    if cpu is not None:
+        for line in lines:
+            if line["op"].endswith("_chain"):
+                line["cpu_baseline"] = cpu(w, line["op"])
+    return lines
+
+
+def _sum_chain(wr, payload, A):
+    wa, ra = wr
+    return causal_sum_lookup(wa, payload, ra, address_space=A)
+
+
 def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
                  cpu: Optional[Callable] = None) -> List[dict]:
     w = workloads.cfg5(dev, steps=steps)
@@ -132,9 +212,14 @@ def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
     return lines
 
 
-def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None) -> List[dict]:
+PARTS = ("tapes", "addresses", "decode")
+
+
+def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
+        parts=PARTS) -> List[dict]:
+    """Runs the named parts of the suite (all by default) and returns the lines."""
     lines: List[dict] = []
-    tapes = [
+    tapes = [] if "tapes" not in parts else [
         lambda: workloads.cfg1(dev, "1"),
         lambda: workloads.cfg1(dev, "1b"),
         lambda: workloads.cfg2(dev, torch.float32),
@@ -150,16 +235,33 @@ def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None) -> L
             lines.append(line)
         del w
         torch.cuda.empty_cache()
-    for line in decode_lines(dev, cpu=cpu):
+    sources = [] if "addresses" not in parts else [
+        (lambda: workloads.cfg1(dev, "1"), False),
+        (lambda: workloads.cfg2(dev, torch.bfloat16), False),
+        (lambda: workloads.cfg3_logits(dev), True),
+    ]
+    for make, with_sum in sources:
+        w = make()
+        for line in address_lines(w, iters, cpu, with_sum):
+            print(json.dumps(line), flush=True)
+            lines.append(line)
+        del w
+        torch.cuda.empty_cache()
+    for line in decode_lines(dev, cpu=cpu) if "decode" in parts else []:
         print(json.dumps(line), flush=True)
         lines.append(line)
     return lines
 
 
 def main(argv=None) -> None:
+    """``python -m ravel_em.suite [part ...]`` with parts among tapes, addresses, decode."""
     if not torch.cuda.is_available():
         sys.exit("the suite needs a ROCm GPU")
-    run(torch.device("cuda", 0))
+    parts = (argv if argv is not None else sys.argv[1:]) or PARTS
+    bad = [p for p in parts if p not in PARTS]
+    if bad:
+        sys.exit(f"unknown suite parts {bad}; choose from {PARTS}")
+    run(torch.device("cuda", 0), parts=tuple(parts))
 
 
 if __name__ == "__main__":

@@ -23,6 +23,8 @@ from typing import Optional
 
 import torch
 
+from .addressing import LayerAddresses
+
 Tensor = torch.Tensor
 BOS = 257  # RavelConfig.bos_token_id (ravel_lm/config.py)
 
@@ -35,6 +37,8 @@ class Workload:
     payload: Tensor
     address_space: int
     k: int
+    # the layer inputs the addresses come from (token ids / addressor logits)
+    source: Optional[LayerAddresses] = None
 
     @property
     def shape(self):
@@ -104,7 +108,8 @@ def cfg1(device="cuda", variant: str = "1") -> Workload:
         A = 512
         addr = literal_addresses(toks, address_space=A, n_heads=H)
     payload = _normal((B, T, H, D), g, torch.float32)
-    return Workload(f"cfg{variant}", addr, None, payload, A, 4)
+    src = LayerAddresses(toks, H, BOS) if variant != "1b" else None
+    return Workload(f"cfg{variant}", addr, None, payload, A, 4, src)
 
 
 def cfg2(device="cuda", dtype: torch.dtype = torch.float32) -> Workload:
@@ -113,7 +118,8 @@ def cfg2(device="cuda", dtype: torch.dtype = torch.float32) -> Workload:
     toks = zipf((B, T), 1024, g)
     addr = literal_addresses(toks, address_space=A, n_heads=H)
     payload = _normal((B, T, H, D), g, dtype)
-    return Workload(f"cfg2_{str(dtype).split('.')[-1]}", addr, None, payload, A, 8)
+    return Workload(f"cfg2_{str(dtype).split('.')[-1]}", addr, None, payload, A, 8,
+                    LayerAddresses(toks, H, BOS))
 
 
 def product_code_addresses(B: int, T: int, H: int, g: torch.Generator, codebook: int = 64) -> Tensor:
@@ -134,6 +140,26 @@ def cfg3(device="cuda", B: int = 64, T: int = 4096) -> Workload:
     read = product_code_addresses(B, T, H, g)
     payload = _normal((B, T, H, D), g, torch.bfloat16)
     return Workload("cfg3", write, read, payload, 4096, 4)
+
+
+def cfg3_logits(device="cuda", B: int = 64, T: int = 4096) -> Workload:
+    """cfg3 as the memory layer sees it: bf16 N(0,1) write and read addressor
+    logits side by side in one packed projection row [B, T, 2 * H*2*64]
+    (ravel_lm/model.py:325-341), decoded inside the lookup.  ``write``/``read``
+    hold the same addresses decoded by torch.argmax on the device."""
+    g = _gen(device, 1013)
+    H, D, Q, S, A = 8, 64, 2, 64, 4096
+    n = H * Q * S
+    packed = torch.empty(B, T, 2 * n, dtype=torch.bfloat16, device=g.device)
+    for b in range(B):
+        packed[b] = torch.randn(T, 2 * n, generator=g, device=g.device).to(torch.bfloat16)
+    wl, rl = packed[..., :n], packed[..., n:]
+    mult = torch.tensor([1, S], device=g.device)
+    write = (wl.reshape(B, T, H, Q, S).argmax(-1) * mult).sum(-1).remainder(A)
+    read = (rl.reshape(B, T, H, Q, S).argmax(-1) * mult).sum(-1).remainder(A)
+    payload = _normal((B, T, H, D), g, torch.bfloat16)
+    src = LayerAddresses(None, 0, BOS, wl, rl, H, Q, S)
+    return Workload("cfg3_logits", write, read, payload, A, 4, src)
 
 
 def cfg4(device="cuda", adversarial: bool = False, B: int = 4, T: int = 65536) -> Workload:

@@ -37,7 +37,7 @@ def test_binding_table_matches_header():
 
 
 def test_abi_version():
-    assert nat.library().ravel_em_abi_version() == 1
+    assert nat.library().ravel_em_abi_version() == 2
 
 
 @pytest.mark.parametrize("shape", [(1, 2048, 3, 1024), (1024, 65536, 64, 65536), (8, 256, 4, 512),
