@@ -16,7 +16,7 @@
 // units, then a butterfly of xor shuffles merges the G candidates under a
 // strict total order (NaN above numbers, then the larger value, then the
 // smaller index), so every lane of the group ends with the argmax that
-// torch.argmax returns (cfg3, 2 x 537 MB of bf16 logits: about 100 us a side,
+// torch.argmax returns (cfg3, 2 x 537 MB of bf16 logits: about 114 us a side,
 // against 78 us for a plain read of the same bytes).  A group takes several heads per round and loads all
 // their units before the first compare.  Logit rows that are not whole aligned
 // 16-byte units (or more than 4 codebooks, or units per codebook not a power

@@ -244,7 +244,9 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   stage_end(kStageSort, s);
   if (e != hipSuccess) return hip_fail(e, "sort");
   stage_begin(kStageResolve, s);
-  if (link) {
+  if (link && sorted && link_rows_applies(tp, (int)k, sizeof(U))) {
+    e = link_rows<U>(sorted, tp, (int)k, src, s);
+  } else if (link) {
     if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {
@@ -271,7 +273,9 @@ int resolve_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
                               link && k == 1 ? src_seg : nullptr);
   if (e != hipSuccess) return hip_fail(e, "sort");
-  if (link) {
+  if (link && sorted && link_rows_applies(tp, (int)k, sizeof(U))) {
+    e = link_rows<U>(sorted, tp, (int)k, src, s);
+  } else if (link) {
     if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
     if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
   } else {

@@ -213,6 +213,11 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 // search_reads writes record-major ([B,T,C,k]).
 template <typename U>
 hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s);
+// read == write with every head of a batch row in LDS (link_rows_applies):
+// the sources record-major ([B,T,C,k]) in one kernel.
+bool link_rows_applies(const Tape& tp, int k, size_t key_bytes);
+template <typename U>
+hipError_t link_rows(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s);
 template <typename U>
 hipError_t search_reads(const U* sorted, const AddrIn& raddr, const Tape& tp, int k, int32_t* src,
                         int32_t* spos, hipStream_t s);

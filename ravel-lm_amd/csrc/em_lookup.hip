@@ -495,6 +495,69 @@ __global__ __launch_bounds__(256) void src_transpose_pow2_kernel(const int32_t* 
   }
 }
 
+// read == write, short tapes: every head's sorted segment of one batch row
+// (C*T keys, one contiguous run of the segment-major keys) sits in LDS, and one
+// block per (b, chunk of tchunk times) finds, for each key whose time falls in
+// its chunk, the up to k previous keys of the same address (its sorted
+// neighbours), writes their record ids into an LDS tile [tchunk][C][k] that
+// starts at -1, and stores the tile: the chunk of the record-major sources
+// [B,T,C,k] is one contiguous run, written with coalesced stores.  No global
+// scatter and no transpose.
+constexpr int kRowsKeyBytes = 32 * 1024;  // keys of one batch row (with the chunk: <= 64 KiB of LDS)
+constexpr int kRowsOutBytes = 32 * 1024;  // sources of one chunk
+
+template <typename U>
+__global__ __launch_bounds__(256) void link_rows_lds_kernel(const U* __restrict__ sorted,
+                                                           int64_t T, int64_t C, int k,
+                                                           int tbits, int tchunk, int nchunk,
+                                                           int64_t nlogical,
+                                                           int32_t* __restrict__ src) {
+  extern __shared__ __align__(16) unsigned char rows_lds[];
+  const int Ci = (int)C, Ti = (int)T;
+  const int nkeys = Ci * Ti;
+  U* keys = (U*)rows_lds;
+  int32_t* out = (int32_t*)(rows_lds + (((size_t)nkeys * sizeof(U) + 15) & ~(size_t)15));
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nlogical) return;  // padding block of the XCD-rounded grid (uniform)
+  const int64_t b = lb / nchunk;
+  const int t0 = (int)(lb - b * nchunk) * tchunk;
+  const int tn = (Ti - t0) < tchunk ? (Ti - t0) : tchunk;
+  const int nout = tn * Ci * k;
+  const U* row = sorted + b * (int64_t)nkeys;
+  const bool vec_in = ((uintptr_t)row & 15) == 0 && (nkeys * (int)sizeof(U)) % 16 == 0;
+  if (vec_in) {
+    const int nv = nkeys * (int)sizeof(U) / 16;
+    for (int i = threadIdx.x; i < nv; i += 256) ((u32x4*)keys)[i] = ((const u32x4*)row)[i];
+  } else {
+    for (int i = threadIdx.x; i < nkeys; i += 256) keys[i] = row[i];
+  }
+  for (int i = threadIdx.x; i < nout; i += 256) out[i] = -1;
+  __syncthreads();
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  for (int c = 0; c < Ci; ++c) {
+    const U* sk = keys + c * Ti;
+    for (int p = threadIdx.x; p < Ti; p += 256) {
+      const U u = sk[p];
+      const int t = (int)(u & tmask);
+      if (t < t0 || t >= t0 + tn) continue;
+      const U a = u >> tbits;
+      int32_t* o = out + ((t - t0) * Ci + c) * k;
+      for (int j = 0; j < k && p - 1 - j >= 0; ++j) {
+        const U uq = sk[p - 1 - j];
+        if ((uq >> tbits) != a) break;
+        o[j] = (int32_t)((b * T + (int64_t)(uq & tmask)) * C + c);
+      }
+    }
+  }
+  __syncthreads();
+  int32_t* dst = src + (b * T + t0) * C * k;
+  if ((Ci * k) % 4 == 0 && ((uintptr_t)src & 15) == 0) {
+    for (int i = threadIdx.x; i < nout / 4; i += 256) ((u32x4*)dst)[i] = ((const u32x4*)out)[i];
+  } else {
+    for (int i = threadIdx.x; i < nout; i += 256) dst[i] = out[i];
+  }
+}
+
 __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n,
                                                      uint8_t v) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -526,6 +589,37 @@ hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s) {
 static bool link_lds_applies(const Tape& tp, int k) {
   const int64_t nchunk = (tp.T + kLinkLdsWords - 1) / kLinkLdsWords;
   return k == 1 && nchunk >= 1 && nchunk <= 8;  // segment read amplification <= 8x
+}
+
+// Chunk length of link_rows_lds_kernel for this tape (0 = the kernel does not
+// apply): the batch row's keys fit kRowsKeyBytes, a power-of-two chunk of
+// sources fits kRowsOutBytes.
+static int rows_chunk(const Tape& tp, int k, size_t key_bytes) {
+  if (tp.T < 1 || tp.C < 1 || (size_t)(tp.C * tp.T) * key_bytes > (size_t)kRowsKeyBytes) return 0;
+  const int64_t per_t = tp.C * (int64_t)k * 4;
+  if (per_t > kRowsOutBytes) return 0;
+  int64_t tc = 1;
+  while (tc * 2 * per_t <= kRowsOutBytes && tc * 2 <= tp.T) tc *= 2;
+  return (int)tc;
+}
+
+bool link_rows_applies(const Tape& tp, int k, size_t key_bytes) {
+  return rows_chunk(tp, k, key_bytes) > 0;
+}
+
+template <typename U>
+hipError_t link_rows(const U* sorted, const Tape& tp, int k, int32_t* src, hipStream_t s) {
+  if (tp.n() == 0) return hipSuccess;
+  const int tc = rows_chunk(tp, k, sizeof(U));
+  if (tc == 0) return hipErrorInvalidValue;
+  const int64_t nchunk = (tp.T + tc - 1) / tc;
+  const int64_t nlogical = tp.B * nchunk;
+  const size_t lds = (((size_t)(tp.C * tp.T) * sizeof(U) + 15) & ~(size_t)15) +
+                     (size_t)tc * tp.C * k * 4;
+  const unsigned grid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
+  link_rows_lds_kernel<U><<<grid, 256, lds, s>>>(sorted, tp.T, tp.C, k, tp.tbits, tc,
+                                                  (int)nchunk, nlogical, src);
+  return hipGetLastError();
 }
 
 template <typename U>
@@ -618,6 +712,8 @@ hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64
 
 template hipError_t link_same<uint32_t>(const uint32_t*, const Tape&, int, int32_t*, hipStream_t);
 template hipError_t link_same<uint64_t>(const uint64_t*, const Tape&, int, int32_t*, hipStream_t);
+template hipError_t link_rows<uint32_t>(const uint32_t*, const Tape&, int, int32_t*, hipStream_t);
+template hipError_t link_rows<uint64_t>(const uint64_t*, const Tape&, int, int32_t*, hipStream_t);
 template hipError_t search_reads<uint32_t>(const uint32_t*, const AddrIn&, const Tape&, int,
                                            int32_t*, int32_t*, hipStream_t);
 template hipError_t search_reads<uint64_t>(const uint64_t*, const AddrIn&, const Tape&, int,

@@ -792,6 +792,11 @@ PackPlan fused_plan(const Tape& tp, size_t key_bytes) {
   if (cc > tp.C) cc = tp.C;
   if (cc * npass * kRadix > kHistWords) cc = kHistWords / (npass * kRadix);
   if (cc < 1) return pl;
+  // Short tapes: fewer heads per pack block until the grid has two blocks per
+  // CU (the heads of one time tile stay on one XCD, so their shared address
+  // rows are read from L2).
+  auto blocks = [&](int64_t c) { return tp.B * ((tp.T + tt - 1) / tt) * ((tp.C + c - 1) / c); };
+  while (cc > 1 && blocks(cc) < 512) cc = (cc + 1) / 2;
   pl.TT = tt;
   pl.CC = (int)cc;
   return pl;

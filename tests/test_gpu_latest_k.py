@@ -118,6 +118,10 @@ SMALL = [
     (2, 9000, 3, 1 << 17, None, None, True, False, 2),  # masked, 3 passes, 2 look-back sweeps
     (1, 65536, 2, 3, None, None, False, False, 1),  # one-chunk link at its longest segment
     (1, 70000, 2, 50, None, None, False, False, 1),  # link in 16384-step chunks (T > 65536)
+    (2, 2048, 4, 5000, None, None, False, False, 8),  # batch-row link at its LDS limit (C*T = 8192)
+    (3, 1000, 8, 1024, None, None, False, False, 5),  # batch-row link, ragged time chunks
+    (2, 1000, 4, (1 << 23) + 5, None, None, False, False, 3),  # batch-row link over 64-bit keys
+    (2, 333, 3, 7, None, None, False, False, 1),  # batch-row link, k = 1, scalar stores
 ]
 
 
