@@ -496,65 +496,116 @@ __global__ __launch_bounds__(256) void src_transpose_pow2_kernel(const int32_t* 
 }
 
 // read == write, short tapes: every head's sorted segment of one batch row
-// (C*T keys, one contiguous run of the segment-major keys) sits in LDS, and one
-// block per (b, chunk of tchunk times) finds, for each key whose time falls in
-// its chunk, the up to k previous keys of the same address (its sorted
-// neighbours), writes their record ids into an LDS tile [tchunk][C][k] that
-// starts at -1, and stores the tile: the chunk of the record-major sources
-// [B,T,C,k] is one contiguous run, written with coalesced stores.  No global
-// scatter and no transpose.
-constexpr int kRowsKeyBytes = 32 * 1024;  // keys of one batch row (with the chunk: <= 64 KiB of LDS)
-constexpr int kRowsOutBytes = 32 * 1024;  // sources of one chunk
+// (C*T keys, one contiguous run of the segment-major keys) sits in LDS.  One
+// block per (b, chunk of tchunk times) first records, for each key whose time
+// falls in its chunk, the key's sorted position at inv[t - t0][c]; then each
+// thread takes output rows (t, c) of the chunk and reads the k sorted
+// neighbours before the row's position at once (independent LDS reads; a
+// neighbour counts while the address matches) and writes the row's k record
+// ids.  The chunk of the record-major sources [B,T,C,k] is one contiguous run,
+// written row by row from consecutive lanes: no global scatter, no transpose.
+constexpr int kRowsKeyBytes = 48 * 1024;  // keys of one batch row
+constexpr int kRowsInvBytes = 16 * 1024;  // sorted positions of one chunk
+constexpr int kRowsThreads = 512;
+constexpr int kRowsBatch = 8;  // staging loads in flight per thread
 
 template <typename U>
-__global__ __launch_bounds__(256) void link_rows_lds_kernel(const U* __restrict__ sorted,
-                                                           int64_t T, int64_t C, int k,
-                                                           int tbits, int tchunk, int nchunk,
-                                                           int64_t nlogical,
-                                                           int32_t* __restrict__ src) {
+__global__ __launch_bounds__(kRowsThreads) void link_rows_lds_kernel(const U* __restrict__ sorted,
+                                                                    int64_t T, int64_t C, int k,
+                                                                    int tbits, int tchunk,
+                                                                    int nchunk, int64_t nlogical,
+                                                                    int32_t* __restrict__ src) {
   extern __shared__ __align__(16) unsigned char rows_lds[];
   const int Ci = (int)C, Ti = (int)T;
   const int nkeys = Ci * Ti;
   U* keys = (U*)rows_lds;
-  int32_t* out = (int32_t*)(rows_lds + (((size_t)nkeys * sizeof(U) + 15) & ~(size_t)15));
+  int32_t* inv = (int32_t*)(rows_lds + (((size_t)nkeys * sizeof(U) + 15) & ~(size_t)15));
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   if (lb >= nlogical) return;  // padding block of the XCD-rounded grid (uniform)
   const int64_t b = lb / nchunk;
   const int t0 = (int)(lb - b * nchunk) * tchunk;
   const int tn = (Ti - t0) < tchunk ? (Ti - t0) : tchunk;
-  const int nout = tn * Ci * k;
   const U* row = sorted + b * (int64_t)nkeys;
   const bool vec_in = ((uintptr_t)row & 15) == 0 && (nkeys * (int)sizeof(U)) % 16 == 0;
+  // Staging: every load of a batch is issued before its stores (the index is
+  // clamped instead of tested, so no wait lands between the loads).
   if (vec_in) {
     const int nv = nkeys * (int)sizeof(U) / 16;
-    for (int i = threadIdx.x; i < nv; i += 256) ((u32x4*)keys)[i] = ((const u32x4*)row)[i];
+    for (int i0 = 0; i0 < nv; i0 += kRowsThreads * kRowsBatch) {
+      u32x4 x[kRowsBatch];
+#pragma unroll
+      for (int m = 0; m < kRowsBatch; ++m) {
+        const int i = i0 + m * kRowsThreads + (int)threadIdx.x;
+        x[m] = ((const u32x4*)row)[i < nv ? i : nv - 1];
+      }
+#pragma unroll
+      for (int m = 0; m < kRowsBatch; ++m) {
+        const int i = i0 + m * kRowsThreads + (int)threadIdx.x;
+        if (i < nv) ((u32x4*)keys)[i] = x[m];
+      }
+    }
   } else {
-    for (int i = threadIdx.x; i < nkeys; i += 256) keys[i] = row[i];
-  }
-  for (int i = threadIdx.x; i < nout; i += 256) out[i] = -1;
-  __syncthreads();
-  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
-  for (int c = 0; c < Ci; ++c) {
-    const U* sk = keys + c * Ti;
-    for (int p = threadIdx.x; p < Ti; p += 256) {
-      const U u = sk[p];
-      const int t = (int)(u & tmask);
-      if (t < t0 || t >= t0 + tn) continue;
-      const U a = u >> tbits;
-      int32_t* o = out + ((t - t0) * Ci + c) * k;
-      for (int j = 0; j < k && p - 1 - j >= 0; ++j) {
-        const U uq = sk[p - 1 - j];
-        if ((uq >> tbits) != a) break;
-        o[j] = (int32_t)((b * T + (int64_t)(uq & tmask)) * C + c);
+    for (int i0 = 0; i0 < nkeys; i0 += kRowsThreads * kRowsBatch) {
+      U x[kRowsBatch];
+#pragma unroll
+      for (int m = 0; m < kRowsBatch; ++m) {
+        const int i = i0 + m * kRowsThreads + (int)threadIdx.x;
+        x[m] = row[i < nkeys ? i : nkeys - 1];
+      }
+#pragma unroll
+      for (int m = 0; m < kRowsBatch; ++m) {
+        const int i = i0 + m * kRowsThreads + (int)threadIdx.x;
+        if (i < nkeys) keys[i] = x[m];
       }
     }
   }
   __syncthreads();
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  // Every (t, c) of the chunk has exactly one key (no mask on this path).
+  for (int c = 0; c < Ci; ++c) {
+    const U* sk = keys + c * Ti;
+    for (int p = threadIdx.x; p < Ti; p += kRowsThreads) {
+      const int t = (int)(sk[p] & tmask);
+      if (t >= t0 && t < t0 + tn) inv[(t - t0) * Ci + c] = p;
+    }
+  }
+  __syncthreads();
   int32_t* dst = src + (b * T + t0) * C * k;
-  if ((Ci * k) % 4 == 0 && ((uintptr_t)src & 15) == 0) {
-    for (int i = threadIdx.x; i < nout / 4; i += 256) ((u32x4*)dst)[i] = ((const u32x4*)out)[i];
-  } else {
-    for (int i = threadIdx.x; i < nout; i += 256) dst[i] = out[i];
+  const int nrow = tn * Ci;
+  // k a multiple of 4 (and an aligned base): rows go out in 16-byte units.
+  const bool vec_out = k % 4 == 0 && ((uintptr_t)src & 15) == 0;
+  for (int r = threadIdx.x; r < nrow; r += kRowsThreads) {
+    const int c = r % Ci;
+    const int p = inv[r];
+    const U* sk = keys + c * Ti;
+    const U a = sk[p] >> tbits;
+    const int32_t base = (int32_t)((b * T) * C + c);
+    bool alive = true;
+    int32_t* o = dst + (int64_t)r * k;
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      U nb[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {  // all reads first (clamped into the segment)
+        const int q = p - 1 - j0 - m;
+        nb[m] = sk[q >= 0 ? q : 0];
+      }
+      int32_t v[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        alive = alive && p - 1 - j0 - m >= 0 && (nb[m] >> tbits) == a;
+        v[m] = alive ? base + (int32_t)(nb[m] & tmask) * Ci : -1;
+      }
+      if (vec_out && j0 + 8 <= k) {  // whole 16-byte units of the row
+        *(u32x4*)(o + j0) = u32x4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        *(u32x4*)(o + j0 + 4) = u32x4{(uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]};
+      } else if (vec_out && j0 + 4 <= k) {
+        *(u32x4*)(o + j0) = u32x4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+      } else {
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+          if (j0 + m < k) o[j0 + m] = v[m];
+      }
+    }
   }
 }
 
@@ -592,14 +643,17 @@ static bool link_lds_applies(const Tape& tp, int k) {
 }
 
 // Chunk length of link_rows_lds_kernel for this tape (0 = the kernel does not
-// apply): the batch row's keys fit kRowsKeyBytes, a power-of-two chunk of
-// sources fits kRowsOutBytes.
+// apply): the batch row's keys fit kRowsKeyBytes, the sorted positions of a
+// power-of-two chunk fit kRowsInvBytes.
 static int rows_chunk(const Tape& tp, int k, size_t key_bytes) {
   if (tp.T < 1 || tp.C < 1 || (size_t)(tp.C * tp.T) * key_bytes > (size_t)kRowsKeyBytes) return 0;
-  const int64_t per_t = tp.C * (int64_t)k * 4;
-  if (per_t > kRowsOutBytes) return 0;
+  const int64_t per_t = tp.C * 4;  // sorted positions of one time step
+  if (per_t > kRowsInvBytes || k < 1) return 0;
+  // Chunks small enough to give every CU a block, large enough that the
+  // batch row's keys (read once per chunk) stay a small part of the traffic.
   int64_t tc = 1;
-  while (tc * 2 * per_t <= kRowsOutBytes && tc * 2 <= tp.T) tc *= 2;
+  while (tc * 2 * per_t <= kRowsInvBytes && tc * 2 <= tp.T) tc *= 2;
+  while (tc > 64 && tp.B * ((tp.T + tc - 1) / tc) < 256) tc /= 2;
   return (int)tc;
 }
 
@@ -615,9 +669,9 @@ hipError_t link_rows(const U* sorted, const Tape& tp, int k, int32_t* src, hipSt
   const int64_t nchunk = (tp.T + tc - 1) / tc;
   const int64_t nlogical = tp.B * nchunk;
   const size_t lds = (((size_t)(tp.C * tp.T) * sizeof(U) + 15) & ~(size_t)15) +
-                     (size_t)tc * tp.C * k * 4;
+                     (size_t)tc * tp.C * 4;
   const unsigned grid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
-  link_rows_lds_kernel<U><<<grid, 256, lds, s>>>(sorted, tp.T, tp.C, k, tp.tbits, tc,
+  link_rows_lds_kernel<U><<<grid, kRowsThreads, lds, s>>>(sorted, tp.T, tp.C, k, tp.tbits, tc,
                                                   (int)nchunk, nlogical, src);
   return hipGetLastError();
 }
