@@ -10,16 +10,28 @@
 //   out[n, m] = sum_k A[n, k] * W[m, k],   n = b*T + t, k = c*P + p,
 //   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
 //
-// Tiles: a block (8 waves) computes kRows rows x kCols columns over K in chunks
-// of kChunk; wave (g, h) owns rows [64g, 64g+64) and columns [64h, 64h+64).  A chunk's A tile is gathered in 16-byte units (8 values;
-// P % 8 == 0 keeps a unit inside one head), W's tile is read row-major, both
-// go to LDS with rows padded to kLds elements (144 bytes: the 16 rows that one
-// MFMA operand read touches land in distinct banks).  A wave runs 4 x 4 tiles
-// of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to the
-// payload dtype.  Operand lane layout (checked on the device): A lane l holds
-// row l%16, k (l/16)*8 .. +7; B lane l holds column l%16, the same k; the
+// Tiles: a block (8 waves, one block per CU) computes kRows rows x kCols
+// columns over K in chunks of kChunk; wave (g, h) owns rows [64g, 64g+64) and
+// columns [64h, 64h+64).  A chunk's A tile is gathered in 16-byte units (8
+// values; P % 8 == 0 keeps a unit inside one head), W's tile is read row-major,
+// both go to LDS with rows padded to kLds elements (144 bytes: the 16 rows that
+// one MFMA operand read touches land in distinct banks).  A wave runs 4 x 4
+// tiles of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to
+// the payload dtype.  Operand lane layout (checked on the device): A lane l
+// holds row l%16, k (l/16)*8 .. +7; B lane l holds column l%16, the same k; the
 // result lane l holds column l%16, rows (l/16)*4 .. +3.  The epilogue stages
 // the tile in LDS and writes whole 16-byte units of the output rows.
+//
+// Pipelining: kStages register sets hold the next chunks' units while the
+// current chunk multiplies out of LDS.  Every load is unconditional (a missing
+// or out-of-range unit reads kZeroUnit, a zero in global memory, instead of
+// being skipped or selected) and the chunk loop runs whole rounds of kStages
+// with no branch around its loads, so the compiler's wait counts let the
+// prefetched chunks stay in flight across the barriers (a conditional load or
+// a select on the loaded value makes it wait for every outstanding load).
+// Two stages measured best (three and four: more registers, no gain).
+
+#include <type_traits>
 
 #include "em_common.h"
 
@@ -33,6 +45,7 @@ constexpr int kSrcLds = 32;  // heads whose sources a block stages in LDS
 constexpr int kCols = 256;
 constexpr int kChunk = 64;
 constexpr int kLds = kChunk + 8;
+constexpr int kStages = 2;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -60,10 +73,12 @@ __device__ __forceinline__ uint16_t round16(float x) {
     return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
 }
 
-template <bool F16>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void gather_gemm_kernel(
+__device__ u32x4 kZeroUnit = {0u, 0u, 0u, 0u};  // never written: the unit a missing row reads
+
+template <bool F16, bool SRC_LDS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gather_gemm_kernel(
     const uint16_t* __restrict__ payload, const int32_t* __restrict__ src,
-    const uint16_t* __restrict__ W, int64_t NR, int C, int P, int M, int64_t nsrc,
+    const uint16_t* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
     uint16_t* __restrict__ out) {
   constexpr int RT = 4;  // 16-row tiles per wave (64 rows)
   __shared__ __align__(16) uint16_t As[kRows * kLds];
@@ -75,8 +90,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
   const int K = C * P;
   // The block's sources [kRows][C] (one contiguous run) go to LDS once, so a
   // chunk's gather costs one memory round trip.
-  const bool src_lds = C <= kSrcLds;
-  if (src_lds) {
+  if (SRC_LDS) {
     const int64_t nrow = (NR - row0) < kRows ? (NR - row0) : kRows;
     for (int i = tid; i < nrow * C; i += kThreads) Ss[i] = src[row0 * C + i];
     __syncthreads();
@@ -91,60 +105,73 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
   // multiplies out of LDS.
   constexpr int AU = kRows * 8 / kThreads;
   constexpr int BU = kCols * 8 / kThreads;
-  u32x4 av[AU], bv[BU];
-  auto load_chunk = [&](int k0) {
+  u32x4 av[kStages][AU], bv[kStages][BU];
+  const u32x4* zero = &kZeroUnit;
+  auto load_chunk = [&](int k0, u32x4 (&a)[AU], u32x4 (&bb)[BU]) {
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
       const int u = tid + kThreads * q;
       const int r = u >> 3, piece = u & 7;
       const int k = k0 + piece * 8;
       const int64_t n = row0 + r;
-      av[q] = u32x4{0u, 0u, 0u, 0u};
-      if (n < NR && k < K) {
-        const int c = k / P;
-        const int32_t s = src_lds ? Ss[r * C + c] : src[n * C + c];
-        if (s >= 0 && s < nsrc) av[q] = *(const u32x4*)(payload + (int64_t)s * P + (k - c * P));
-      }
+      // Branch-free: an out-of-range or missing row reads a zero unit.
+      const bool in = n < NR && k < K;
+      const int kc = in ? k : 0;
+      const int c = (int)fdiv((uint32_t)kc, byP);
+      const int32_t s = SRC_LDS ? Ss[r * C + c] : src[(in ? n : row0) * C + c];
+      const bool ok = in && s >= 0 && s < nsrc;
+      a[q] = *(ok ? (const u32x4*)(payload + (int64_t)s * P + (kc - c * P)) : zero);
     }
 #pragma unroll
     for (int q = 0; q < BU; ++q) {
       const int u = tid + kThreads * q;
       const int m = u >> 3, piece = u & 7;
       const int k = k0 + piece * 8;
-      bv[q] = (m < M && k < K) ? *(const u32x4*)(W + (int64_t)m * K + k) : u32x4{0u, 0u, 0u, 0u};
+      const bool in = m < M && k < K;
+      bb[q] = *(in ? (const u32x4*)(W + (int64_t)m * K + k) : zero);
     }
   };
-  load_chunk(0);
-  for (int k0 = 0; k0 < K; k0 += kChunk) {
+  // Chunks rounded up to whole rounds of kStages (chunks past K read zero
+  // units), so the loop body is straight-line: every stage issues its loads.
+  const int nch = (K + kChunk - 1) / kChunk;
+  const int nchp = (nch + kStages - 1) / kStages * kStages;
 #pragma unroll
-    for (int q = 0; q < AU; ++q) {
-      const int u = tid + kThreads * q;
-      *(u32x4*)&As[(u >> 3) * kLds + (u & 7) * 8] = av[q];
-    }
+  for (int st = 0; st < kStages; ++st) load_chunk(st * kChunk, av[st], bv[st]);
+  for (int c0 = 0; c0 < nchp; c0 += kStages) {
 #pragma unroll
-    for (int q = 0; q < BU; ++q) {
-      const int u = tid + kThreads * q;
-      *(u32x4*)&Bs[(u >> 3) * kLds + (u & 7) * 8] = bv[q];
-    }
-    __syncthreads();
-    if (k0 + kChunk < K) load_chunk(k0 + kChunk);
-    if (wave_live) {
+    for (int st = 0; st < kStages; ++st) {
+      const int ch = c0 + st;
 #pragma unroll
-      for (int ks = 0; ks < kChunk / 32; ++ks) {
-        const int kk = ks * 32 + (lane >> 4) * 8;
-        u32x4 b[4];
+      for (int q = 0; q < AU; ++q) {
+        const int u = tid + kThreads * q;
+        *(u32x4*)&As[(u >> 3) * kLds + (u & 7) * 8] = av[st][q];
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          b[j] = *(const u32x4*)&Bs[(wcol * 64 + j * 16 + (lane & 15)) * kLds + kk];
+      for (int q = 0; q < BU; ++q) {
+        const int u = tid + kThreads * q;
+        *(u32x4*)&Bs[(u >> 3) * kLds + (u & 7) * 8] = bv[st][q];
+      }
+      __syncthreads();
+      // Always issued (past the end it re-reads the last chunk, unused).
+      load_chunk((ch + kStages < nchp ? ch + kStages : nchp - 1) * kChunk, av[st], bv[st]);
+      if (wave_live) {
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-          const u32x4 a = *(const u32x4*)&As[(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
+        for (int ks = 0; ks < kChunk / 32; ++ks) {
+          const int kk = ks * 32 + (lane >> 4) * 8;
+          u32x4 b[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
+          for (int j = 0; j < 4; ++j)
+            b[j] = *(const u32x4*)&Bs[(wcol * 64 + j * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+          for (int i = 0; i < RT; ++i) {
+            const u32x4 a = *(const u32x4*)&As[(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
+          }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
   // Epilogue: round to 16 bits and stage the tile in the (now free) B buffer,
   // kRows/2 rows at a time (padded rows of kCols + 8), then write 16-byte units.
@@ -191,14 +218,19 @@ hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, i
   const int64_t blocks = (NR + kRows - 1) / kRows;
   if (blocks > INT32_MAX || C * P > INT32_MAX) return hipErrorInvalidValue;
   const int64_t nsrc = NR * C;
-  if (dtype == kF16)
-    gather_gemm_kernel<true><<<(unsigned)blocks, kThreads, 0, s>>>(
-        (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
-        (uint16_t*)out);
-  else
-    gather_gemm_kernel<false><<<(unsigned)blocks, kThreads, 0, s>>>(
-        (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, (int)M, nsrc,
-        (uint16_t*)out);
+  const FastDiv byP = make_fastdiv((uint32_t)P);
+  auto go = [&](auto f16, auto src_lds) {
+    gather_gemm_kernel<decltype(f16)::value, decltype(src_lds)::value>
+        <<<(unsigned)blocks, kThreads, 0, s>>>((const uint16_t*)payload, src, (const uint16_t*)W, NR,
+                                              (int)C, (int)P, byP, (int)M, nsrc, (uint16_t*)out);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (dtype == kF16) {
+    if (C <= kSrcLds) go(T_{}, T_{}); else go(T_{}, F_{});
+  } else {
+    if (C <= kSrcLds) go(F_{}, T_{}); else go(F_{}, F_{});
+  }
   return hipGetLastError();
 }
 
