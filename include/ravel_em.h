@@ -81,9 +81,25 @@ typedef struct ravel_em_addr_gen {
   int32_t codebook_size;
   int64_t logits_stride_b;    /* element strides of logits over b and t */
   int64_t logits_stride_t;
+  /* Tokens before t = 0, for the bigram/trigram heads: history[b][history_len-1]
+     is the token at t = -1 (the newest last, as the reference's token_history
+     [prev2, prev1]); earlier than the history is bos_token_id.  NULL with
+     history_len 0 is a sequence start (literal_addresses_from_tokens). */
+  const void* history;        /* device [B, history_len], token_dtype */
+  int32_t history_len;
+  int32_t reserved;
+  int64_t history_stride_b;
+  int64_t history_stride_t;
+  int64_t position_offset;    /* the token/position heads (j >= 3) use t + position_offset */
 } ravel_em_addr_gen;
 
 /*
+ * With T = 1, token_ids [B] and the reference's token_history [B, 2] as the
+ * history, position_offset = position and logits [B, N], a descriptor is the
+ * address production of one decode step, RavelMemoryLayer.step
+ * (ravel_lm/model.py:401-419: literal_addresses_step, :234-263, then the
+ * addressors' decode); ravel_em_cache_step takes such descriptors.
+ *
  * The addresses of a descriptor as a [B,T,C] tensor (out_dtype RAVEL_EM_INT64
  * or RAVEL_EM_INT32), in [0, A): torch.cat([literal_addresses_from_tokens(...),
  * _decode_codes(...)], -1) of ravel_lm/model.py:333-343 in one kernel.
@@ -139,8 +155,8 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
  * causal_last_k_lookup forward (ravel_lm/ravel_memory.py:52-176).
  *   write_addr, read_addr [B,T,C] int32/int64 (read_addr NULL = write_addr),
  *   or ravel_em_addr_gen descriptors with RAVEL_EM_ADDR_GEN (as in every entry
- *   point below that takes addr_dtype, except the decode cache's read, write
- *   and step),
+ *   point below that takes addr_dtype, except the decode cache's read and
+ *   write),
  *   write_mask [B,T] bool or NULL, payload [B,T,C,D].
  *   out_values [B,T,C,k,D] (payload dtype), out_mask [B,T,C,k] bool,
  *   out_src [B,T,C,k] int32 source record index or -1 (NULL = not wanted).
@@ -236,7 +252,9 @@ int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr
  * read  (ravel_memory.py:271-281): out_values [B,C,k,D], out_mask [B,C,k].
  * write (ravel_memory.py:283-292): shift-insert payload [B,C,D] at slot 0.
  * step: read at read_addr, then write at write_addr, in one launch
- *   (RavelMemoryLayer.step order, ravel_lm/model.py:421-424).
+ *   (RavelMemoryLayer.step order, ravel_lm/model.py:421-424).  With
+ *   addr_dtype RAVEL_EM_ADDR_GEN, read_addr and write_addr are decode-step
+ *   descriptors (T = 1) and the kernel produces the [B,C] addresses itself.
  */
 int ravel_em_cache_read(const void* values, const uint8_t* filled, const void* addr,
                         int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,

@@ -4,6 +4,7 @@ TEST INFRASTRUCTURE ONLY.  Plain Python loops over small inputs, one function
 per reference routine:
 
   literal_addresses   literal_addresses_from_tokens, ravel_lm/model.py:195-231
+  literal_addresses_step  its decode-step form, ravel_lm/model.py:234-263
   product_codes       ProductCodeAddressor.forward's decode, model.py:177-187,
                       and RavelMemoryLayer._decode_codes, model.py:303-307
   layer_addresses     the write/read assembly of RavelMemoryLayer.forward,
@@ -55,6 +56,35 @@ def literal_addresses(tokens: Sequence[Sequence[int]], *, address_space: int, n_
                 heads.append(_i64(h) % A)
             orow.append(heads)
         out.append(orow)
+    return out
+
+
+def literal_addresses_step(tokens: Sequence[int], history: Sequence[Sequence[int]], *,
+                           address_space: int, n_heads: int, position: int,
+                           bos_token_id: int) -> List[List[int]]:
+    """[B][n_heads] addresses of ravel_lm/model.py:234-263 for one decode step:
+    prev1 is the last history column (bos_token_id when the history is empty),
+    prev2 the one before it (bos_token_id when there are fewer than two), and
+    the token/position heads use `position`."""
+    A = address_space
+    out = []
+    for b, x in enumerate(tokens):
+        h = list(history[b]) if history else []
+        p1 = int(h[-1]) if len(h) >= 1 else bos_token_id
+        p2 = int(h[-2]) if len(h) >= 2 else bos_token_id
+        x = int(x)
+        heads = []
+        for j in range(n_heads):
+            if j == 0:
+                v = x
+            elif j == 1:
+                v = p1 * 257 + x * 131 + 17
+            elif j == 2:
+                v = p2 * 65537 + p1 * 257 + x * 131 + 31
+            else:
+                v = x * (1009 + 2 * j) + int(position) * (9176 + j) + j * 97
+            heads.append(_i64(v) % A)
+        out.append(heads)
     return out
 
 

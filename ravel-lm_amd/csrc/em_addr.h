@@ -13,8 +13,10 @@
 //       1  prev1*257 + tok*131 + 17
 //       2  prev2*65537 + prev1*257 + tok*131 + 31
 //       j  tok*(1009+2j) + t*(9176+j) + j*97        (j >= 3)
-//     with prev1/prev2 the tokens at t-1/t-2 (bos_token_id before t = 0),
-//     int64 arithmetic (two's-complement wrap), Python remainder by A;
+//     with prev1/prev2 the tokens at t-1/t-2 (before t = 0 the caller's token
+//     history, newest last, then bos_token_id) and t counted from the
+//     caller's position offset (model.py:234-263 for one decode step), int64
+//     arithmetic (two's-complement wrap), Python remainder by A;
 //   heads c >= n_lit, product codes (ravel_lm/model.py:177-187, :303-307):
 //     code_q = argmax over codebook q's cbs logits (first maximum; a NaN
 //     counts as the maximum, the first NaN wins), address
@@ -57,11 +59,20 @@ struct GenAddr {
   int64_t lsb, lst;
   int64_t A;
   int tok64, n_lit, n_learned, ldt, ncb, cbs;
+  const void* hist;
+  int64_t hsb, hst, pos_off;
+  int hist_len;
 
+  __device__ __forceinline__ int64_t load_token(const void* p, int64_t i) const {
+    return tok64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
+  }
+
+  // Token at time t of row b; before t = 0 the history (newest last), before
+  // that bos_token_id.
   __device__ __forceinline__ int64_t token(int64_t b, int64_t t) const {
-    if (t < 0) return bos;
-    const int64_t i = b * tsb + t * tst;
-    return tok64 ? ((const int64_t*)tok)[i] : (int64_t)((const int32_t*)tok)[i];
+    if (t >= 0) return load_token(tok, b * tsb + t * tst);
+    const int64_t h = hist_len + t;
+    return h >= 0 ? load_token(hist, b * hsb + h * hst) : bos;
   }
 
   __device__ __forceinline__ int64_t literal(int64_t b, int64_t t, int64_t j) const {
@@ -74,7 +85,8 @@ struct GenAddr {
     } else if (j == 2) {
       h = (uint64_t)token(b, t - 2) * 65537u + (uint64_t)token(b, t - 1) * 257u + x * 131u + 31u;
     } else {
-      h = x * (uint64_t)(1009 + 2 * j) + (uint64_t)t * (uint64_t)(9176 + j) + (uint64_t)(j * 97);
+      h = x * (uint64_t)(1009 + 2 * j) + (uint64_t)(t + pos_off) * (uint64_t)(9176 + j) +
+          (uint64_t)(j * 97);
     }
     return py_mod((int64_t)h, A);
   }
@@ -123,6 +135,11 @@ inline GenAddr make_gen(const AddrGen& g, int64_t A) {
   s.ldt = g.lg_dtype;
   s.ncb = g.ncb;
   s.cbs = g.cbs;
+  s.hist = g.history;
+  s.hist_len = g.hist_len;
+  s.hsb = g.hist_sb;
+  s.hst = g.hist_st;
+  s.pos_off = g.pos_off;
   return s;
 }
 

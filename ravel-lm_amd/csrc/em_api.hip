@@ -134,6 +134,14 @@ int addr_in(const void* p, int dt, int64_t C, AddrIn* out) {
   a.cbs = g->codebook_size;
   a.lg_sb = g->logits_stride_b;
   a.lg_st = g->logits_stride_t;
+  if (g->history_len < 0 || (g->history_len > 0 && !g->history && g->n_literal > 0))
+    return fail(RAVEL_EM_EINVAL, "address descriptor: history_len %d without a history",
+                g->history_len);
+  a.history = g->history;
+  a.hist_len = g->n_literal > 0 ? g->history_len : 0;
+  a.hist_sb = g->history_stride_b;
+  a.hist_st = g->history_stride_t;
+  a.pos_off = g->position_offset;
   return RAVEL_EM_OK;
 }
 
@@ -828,13 +836,21 @@ int ravel_em_cache_step(void* values, uint8_t* filled, const void* read_addr,
                         int payload_dtype, int64_t B, int64_t C, int64_t A, int64_t k, int64_t D,
                         void* out_values, uint8_t* out_mask, void* stream) {
   g_err.clear();
-  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D)) return rc;
+  if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D, true)) return rc;
   if (B * C == 0) return RAVEL_EM_OK;
   if (!values || !filled || !read_addr || !write_addr || !payload || !out_values || !out_mask)
     return fail(RAVEL_EM_EINVAL, "null pointer");
-  hipError_t e = cache_step(values, filled, read_addr, write_addr, addr_dtype == kI64, payload,
-                            B * C, A, k, D * dtype_size(payload_dtype), out_values, out_mask,
-                            (hipStream_t)stream);
+  hipError_t e;
+  if (addr_dtype == kAddrGen) {
+    AddrIn r, w;
+    if (int rc = addr_in(read_addr, addr_dtype, C, &r)) return rc;
+    if (int rc = addr_in(write_addr, addr_dtype, C, &w)) return rc;
+    e = cache_step_gen(values, filled, r, w, payload, B, C, A, k, D * dtype_size(payload_dtype),
+                       out_values, out_mask, (hipStream_t)stream);
+  } else {
+    e = cache_step(values, filled, read_addr, write_addr, addr_dtype == kI64, payload, B * C, A,
+                   k, D * dtype_size(payload_dtype), out_values, out_mask, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return hip_fail(e, "cache step");
   return RAVEL_EM_OK;
 }

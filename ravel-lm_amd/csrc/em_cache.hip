@@ -14,6 +14,7 @@
 //  cache_prefill build the cache of a whole tape from its sorted runs: the last
 //                k records of every (b,c,a) stream go to slots 0..k-1.
 
+#include "em_addr.h"
 #include "em_common.h"
 
 namespace rem {
@@ -54,6 +55,27 @@ __global__ __launch_bounds__(256) void cache_read_kernel(const V* __restrict__ v
   }
 }
 
+// Address of cache row bc = b*C + c, clamped to [0, A) (ravel_memory.py:276,
+// :289): from a dense [B, C] tensor, or produced for the decode step (t = 0 of
+// a T = 1 descriptor: the literal families with the caller's token history and
+// position, or the product codes of the step's logits).
+template <typename AT>
+struct RowAddrDense {
+  const AT* p;
+  int64_t A;
+  __device__ __forceinline__ int64_t operator()(int64_t bc) const { return clamp_addr(p, bc, A); }
+};
+
+struct RowAddrGen {
+  GenAddr g;
+  int64_t C;
+  __device__ __forceinline__ int64_t operator()(int64_t bc) const {
+    const int64_t b = bc / C, c = bc - (bc / C) * C;
+    const int64_t a = c < g.n_lit ? g.literal(b, 0, c) : g.product_code(b, 0, c - g.n_lit);
+    return a < 0 ? 0 : (a >= g.A ? g.A - 1 : a);
+  }
+};
+
 // Block layout shared by write and step: `gpb` (b,c) rows per block, `tpr`
 // threads per row, each thread owns row units v = lid, lid+tpr, ...
 struct RowLayout {
@@ -72,10 +94,10 @@ inline RowLayout row_layout(int64_t upr) {
 // slot is read before the batch below overwrites it.
 constexpr int kCacheBatch = 8;
 
-template <typename V, typename AT, bool READ>
+template <typename V, typename RA, bool READ>
 __global__ __launch_bounds__(256) void cache_rw_kernel(
-    V* __restrict__ values, uint8_t* __restrict__ filled, const AT* __restrict__ raddr,
-    const AT* __restrict__ waddr, const V* __restrict__ payload, int64_t BC, int64_t A, int64_t k,
+    V* __restrict__ values, uint8_t* __restrict__ filled, const RA raddr,
+    const RA waddr, const V* __restrict__ payload, int64_t BC, int64_t A, int64_t k,
     int64_t upr, int tpr, int gpb, V* __restrict__ out, uint8_t* __restrict__ omask) {
   constexpr int KB = kCacheBatch;
   const int lid = threadIdx.x % tpr;
@@ -85,8 +107,8 @@ __global__ __launch_bounds__(256) void cache_rw_kernel(
     // One round: both addresses, then every load of the step (read slots,
     // shift sources, payload), then the stores.  A thread owns the same unit
     // of every row in both halves, and lane 0 of the group owns `filled`.
-    const int64_t s0 = active && READ ? (bc * A + clamp_addr(raddr, bc, A)) * k : 0;
-    const int64_t base = active ? (bc * A + clamp_addr(waddr, bc, A)) * k : 0;
+    const int64_t s0 = active && READ ? (bc * A + raddr(bc)) * k : 0;
+    const int64_t base = active ? (bc * A + waddr(bc)) * k : 0;
     const bool mine = active && lid < upr;
     V rv[KB], sv[KB], pv{};
     uint8_t rf[KB], sf[KB];
@@ -132,7 +154,7 @@ __global__ __launch_bounds__(256) void cache_rw_kernel(
   }
   if (READ) {
     if (active) {
-      const int64_t s0 = (bc * A + clamp_addr(raddr, bc, A)) * k;
+      const int64_t s0 = (bc * A + raddr(bc)) * k;
       for (int64_t j0 = 0; j0 < k; j0 += KB) {
         uint8_t f[KB];
 #pragma unroll
@@ -156,7 +178,7 @@ __global__ __launch_bounds__(256) void cache_rw_kernel(
     __syncthreads();  // every read of the cache precedes the shift below
   }
   if (!active) return;
-  const int64_t base = (bc * A + clamp_addr(waddr, bc, A)) * k;
+  const int64_t base = (bc * A + waddr(bc)) * k;
   for (int64_t v = lid; v < upr; v += tpr) {
     const V pv = payload[bc * upr + v];
     for (int64_t hi = k - 1; hi >= 1; hi -= KB) {
@@ -241,13 +263,27 @@ hipError_t cache_rw_t(void* values, uint8_t* filled, const void* raddr, const vo
   const RowLayout L = row_layout(upr);
   const unsigned grid = (unsigned)((BC + L.gpb - 1) / L.gpb);
   if (addr64)
-    cache_rw_kernel<V, int64_t, READ><<<grid, 256, 0, s>>>(
-        (V*)values, filled, (const int64_t*)raddr, (const int64_t*)waddr, (const V*)payload, BC,
-        A, k, upr, L.tpr, L.gpb, (V*)out, omask);
+    cache_rw_kernel<V, RowAddrDense<int64_t>, READ><<<grid, 256, 0, s>>>(
+        (V*)values, filled, RowAddrDense<int64_t>{(const int64_t*)raddr, A},
+        RowAddrDense<int64_t>{(const int64_t*)waddr, A}, (const V*)payload, BC, A, k, upr, L.tpr,
+        L.gpb, (V*)out, omask);
   else
-    cache_rw_kernel<V, int32_t, READ><<<grid, 256, 0, s>>>(
-        (V*)values, filled, (const int32_t*)raddr, (const int32_t*)waddr, (const V*)payload, BC,
-        A, k, upr, L.tpr, L.gpb, (V*)out, omask);
+    cache_rw_kernel<V, RowAddrDense<int32_t>, READ><<<grid, 256, 0, s>>>(
+        (V*)values, filled, RowAddrDense<int32_t>{(const int32_t*)raddr, A},
+        RowAddrDense<int32_t>{(const int32_t*)waddr, A}, (const V*)payload, BC, A, k, upr, L.tpr,
+        L.gpb, (V*)out, omask);
+  return hipGetLastError();
+}
+
+template <typename V>
+hipError_t cache_step_gen_t(void* values, uint8_t* filled, const GenAddr& r, const GenAddr& w,
+                            const void* payload, int64_t BC, int64_t C, int64_t A, int64_t k,
+                            int64_t upr, void* out, uint8_t* omask, hipStream_t s) {
+  const RowLayout L = row_layout(upr);
+  const unsigned grid = (unsigned)((BC + L.gpb - 1) / L.gpb);
+  cache_rw_kernel<V, RowAddrGen, true><<<grid, 256, 0, s>>>(
+      (V*)values, filled, RowAddrGen{r, C}, RowAddrGen{w, C}, (const V*)payload, BC, A, k, upr,
+      L.tpr, L.gpb, (V*)out, omask);
   return hipGetLastError();
 }
 
@@ -329,5 +365,17 @@ template hipError_t cache_prefill<uint32_t>(const uint32_t*, const void*, const 
                                             int64_t, void*, uint8_t*, hipStream_t);
 template hipError_t cache_prefill<uint64_t>(const uint64_t*, const void*, const Tape&, int64_t,
                                             int64_t, void*, uint8_t*, hipStream_t);
+
+hipError_t cache_step_gen(void* values, uint8_t* filled, const AddrIn& raddr, const AddrIn& waddr,
+                          const void* payload, int64_t B, int64_t C, int64_t A, int64_t k,
+                          int64_t row_bytes, void* out, uint8_t* omask, hipStream_t s) {
+  if (B * C == 0) return hipSuccess;
+  if (raddr.kind != kAddrGen || waddr.kind != kAddrGen) return hipErrorInvalidValue;
+  const GenAddr r = make_gen(raddr.gen, A), w = make_gen(waddr.gen, A);
+  const int vb =
+      vec_bytes((uintptr_t)values | (uintptr_t)payload | (uintptr_t)out | (uintptr_t)row_bytes);
+  REM_VEC_DISPATCH(vb, (cache_step_gen_t<V>(values, filled, r, w, payload, B * C, C, A, k,
+                                            row_bytes / vb, out, omask, s)))
+}
 
 }  // namespace rem

@@ -55,6 +55,10 @@ struct AddrGen {
   int lg_dtype = 0;
   int n_learned = 0, ncb = 0, cbs = 0;
   int64_t lg_sb = 0, lg_st = 0;
+  const void* history = nullptr;  // [B, hist_len] tokens before t = 0, newest last
+  int hist_len = 0;
+  int64_t hist_sb = 0, hist_st = 0;
+  int64_t pos_off = 0;  // position of t = 0 for the token/position heads
 };
 
 // One address input of a call: a dense [B, T, C] tensor (kind kI32 / kI64,
@@ -286,6 +290,11 @@ hipError_t cache_write(void* values, uint8_t* filled, const void* addr, bool add
 hipError_t cache_step(void* values, uint8_t* filled, const void* raddr, const void* waddr,
                       bool addr64, const void* payload, int64_t BC, int64_t A, int64_t k,
                       int64_t row_bytes, void* out, uint8_t* omask, hipStream_t s);
+// The step with produced addresses (kAddrGen read and write inputs, T = 1,
+// heads C): each (b, c) row evaluates its own addresses, clamped to [0, A).
+hipError_t cache_step_gen(void* values, uint8_t* filled, const AddrIn& raddr, const AddrIn& waddr,
+                          const void* payload, int64_t B, int64_t C, int64_t A, int64_t k,
+                          int64_t row_bytes, void* out, uint8_t* omask, hipStream_t s);
 template <typename U>
 hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, int64_t k,
                          int64_t row_bytes, void* values, uint8_t* filled, hipStream_t s);

@@ -8,7 +8,8 @@ replaces the reference's fused arm ``triton_fused_latest1_linear``
 produce the memory layer's addresses (ravel_lm/model.py:195-231, :303-307)
 inside their kernels.
 """
-from .addressing import LayerAddresses, literal_addresses_from_tokens, product_code_addresses
+from .addressing import (LayerAddresses, literal_addresses_from_tokens, literal_addresses_step,
+                         product_code_addresses)
 from .fused import fused_latest1_linear
 from .ravel_memory import (
     RavelLayerCache,
@@ -28,6 +29,7 @@ __all__ = [
     "causal_sum_lookup",
     "fused_latest1_linear",
     "literal_addresses_from_tokens",
+    "literal_addresses_step",
     "product_code_addresses",
     "sort_order",
 ]

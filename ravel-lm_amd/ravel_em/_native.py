@@ -41,6 +41,8 @@ class AddrGen(ctypes.Structure):
         ("logits", _vp), ("logits_dtype", _i32), ("n_learned", _i32),
         ("n_codebooks", _i32), ("codebook_size", _i32),
         ("logits_stride_b", _i64), ("logits_stride_t", _i64),
+        ("history", _vp), ("history_len", _i32), ("reserved", _i32),
+        ("history_stride_b", _i64), ("history_stride_t", _i64), ("position_offset", _i64),
     ]
 
 # name -> (restype, argtypes); must list every function of include/ravel_em.h
@@ -144,15 +146,23 @@ def addr_code(dtype: torch.dtype) -> int:
 
 def addr_gen(tokens: Optional[torch.Tensor], n_literal: int, bos_token_id: int,
              logits: Optional[torch.Tensor], n_learned: int, n_codebooks: int,
-             codebook_size: int) -> AddrGen:
+             codebook_size: int, history: Optional[torch.Tensor] = None,
+             position: int = 0) -> AddrGen:
     """Descriptor of produced addresses.  tokens is [B, T] int32/int64, logits
-    [B, T, n_learned * n_codebooks * codebook_size] with a unit last stride;
-    both are read by the kernels through their strides."""
+    [B, T, n_learned * n_codebooks * codebook_size] with a unit last stride,
+    history [B, h] the tokens before t = 0 (newest last, tokens' dtype); all
+    are read by the kernels through their strides.  position is the time of
+    t = 0 for the token/position heads."""
     g = AddrGen()
     if n_literal > 0:
         g.tokens = tokens.data_ptr()
         g.token_dtype = _ADDR_CODES[tokens.dtype]
         g.token_stride_b, g.token_stride_t = tokens.stride(0), tokens.stride(1)
+        if history is not None and history.shape[1] > 0:
+            g.history = history.data_ptr()
+            g.history_len = history.shape[1]
+            g.history_stride_b, g.history_stride_t = history.stride(0), history.stride(1)
+    g.position_offset = int(position)
     g.n_literal = n_literal
     g.bos_token_id = bos_token_id
     if n_learned > 0:

@@ -100,16 +100,17 @@ _latest1_linear.register_autograd(_backward, setup_context=_setup)
 
 
 @torch.library.custom_op("ravel_em::latest1_linear_gen", mutates_args=())
-def _latest1_linear_gen(tokens: Optional[Tensor], write_logits: Optional[Tensor],
-                        read_logits: Optional[Tensor], payloads: Tensor, weight: Tensor,
-                        n_literal: int, bos: int, n_learned: int, ncb: int, cbs: int,
+def _latest1_linear_gen(tokens: Optional[Tensor], history: Optional[Tensor],
+                        write_logits: Optional[Tensor], read_logits: Optional[Tensor],
+                        payloads: Tensor, weight: Tensor, n_literal: int, bos: int,
+                        n_learned: int, ncb: int, cbs: int, position: int,
                         address_space: int) -> Tuple[Tensor, Tensor]:
     B, T, C, P = payloads.shape
     M = weight.shape[0]
     dev = payloads.device
-    w = nat.addr_gen(tokens, n_literal, bos, write_logits, n_learned, ncb, cbs)
+    w = nat.addr_gen(tokens, n_literal, bos, write_logits, n_learned, ncb, cbs, history, position)
     r = None if read_logits is None else nat.addr_gen(tokens, n_literal, bos, read_logits,
-                                                      n_learned, ncb, cbs)
+                                                      n_learned, ncb, cbs, history, position)
     if _mfma_ok(payloads, weight):
         lib = nat.library()
         src = torch.empty(B, T, C, dtype=torch.int32, device=dev)
@@ -123,31 +124,32 @@ def _latest1_linear_gen(tokens: Optional[Tensor], write_logits: Optional[Tensor]
         return out, src
     from .addressing import latest_k_gen
 
-    values, _, s = latest_k_gen(tokens, write_logits, read_logits, payloads, None, n_literal, bos,
-                                n_learned, ncb, cbs, address_space, 1, True)
+    values, _, s = latest_k_gen(tokens, history, write_logits, read_logits, payloads, None,
+                                n_literal, bos, n_learned, ncb, cbs, position, address_space, 1,
+                                True)
     out = torch.matmul(values.reshape(B * T, C * P), weight.t()).reshape(B, T, M)
     return out, s.view(B, T, C)
 
 
 @_latest1_linear_gen.register_fake
-def _latest1_linear_gen_fake(tokens, write_logits, read_logits, payloads, weight, n_literal, bos,
-                             n_learned, ncb, cbs, address_space):
+def _latest1_linear_gen_fake(tokens, history, write_logits, read_logits, payloads, weight,
+                             n_literal, bos, n_learned, ncb, cbs, position, address_space):
     B, T, C, P = payloads.shape
     return (payloads.new_empty(B, T, weight.shape[0]),
             torch.empty(B, T, C, dtype=torch.int32, device=payloads.device))
 
 
 def _setup_gen(ctx, inputs, output):
-    payloads, weight = inputs[3], inputs[4]
+    payloads, weight = inputs[4], inputs[5]
     _, src = output
     ctx.save_for_backward(src, payloads, weight)
-    ctx.chain = inputs[2] is None
+    ctx.chain = inputs[3] is None
     ctx.mark_non_differentiable(src)
 
 
 def _backward_gen(ctx, grad_out, _grad_src):
-    gp, gw = _grads(ctx, grad_out, ctx.needs_input_grad[3], ctx.needs_input_grad[4])
-    return (None, None, None, gp, gw) + (None,) * 6
+    gp, gw = _grads(ctx, grad_out, ctx.needs_input_grad[4], ctx.needs_input_grad[5])
+    return (None, None, None, None, gp, gw) + (None,) * 7
 
 
 _latest1_linear_gen.register_autograd(_backward_gen, setup_context=_setup_gen)
@@ -220,9 +222,9 @@ def _fused_gen(src: LayerAddresses, payloads: Tensor, read_addresses, weight: Te
         raise ValueError("weight must have shape [M, C * P]")
     if address_space <= 0:
         raise ValueError("address_space must be positive")
-    tok, wl, rl = src.tensors()
-    nat.require_device(payloads, weight, tok, wl, rl)
-    out, _ = _latest1_linear_gen(tok, wl, rl, payloads.contiguous(),
+    tok, hist, wl, rl = src.tensors()
+    nat.require_device(payloads, weight, tok, hist, wl, rl)
+    out, _ = _latest1_linear_gen(tok, hist, wl, rl, payloads.contiguous(),
                                  weight.to(payloads.dtype).contiguous(), *src.cfg(),
                                  int(address_space))
     return out

@@ -21,6 +21,7 @@ import torch
 from . import _native as nat
 from . import _ops
 from .addressing import LayerAddresses, last_k_lookup, sum_lookup
+from .addressing import cache_step as _addr_cache_step
 
 Tensor = torch.Tensor
 
@@ -331,8 +332,24 @@ class RavelLayerCache:
         _ops.cache_write(self.values, self.filled, _cache_addresses(addresses),
                          payloads.to(self.values.dtype).contiguous(), self.k)
 
-    def step(self, read_addresses: Tensor, write_addresses: Tensor, payloads: Tensor) -> Tuple[Tensor, Tensor]:
-        """``read(read_addresses)`` then ``write(write_addresses, payloads)`` in one launch."""
+    def step(self, read_addresses: Tensor, write_addresses: Optional[Tensor], payloads: Tensor) -> Tuple[Tensor, Tensor]:
+        """``read(read_addresses)`` then ``write(write_addresses, payloads)`` in one launch.
+
+        ``read_addresses`` may be a LayerAddresses of one decode step (token ids
+        [B], token_history [B, h], position, logits [B, N]; write_addresses
+        None): the kernel then produces both address sets itself, as
+        RavelMemoryLayer.step does before its read and write
+        (ravel_lm/model.py:401-426).
+        """
+        if isinstance(read_addresses, LayerAddresses):
+            if write_addresses is not None:
+                raise ValueError("with LayerAddresses the write addresses come from it; write_addresses must be None")
+            D = payloads.shape[-1]
+            if self.values.shape[-1] != D or payloads.shape[:2] != self.values.shape[:2]:
+                raise ValueError("cache and payload shapes do not match")
+            vals, mask = _addr_cache_step(read_addresses, self.values, self.filled,
+                                          payloads.to(self.values.dtype).contiguous(), self.k)
+            return self._squeeze(vals, mask)
         B, C = read_addresses.shape
         D = payloads.shape[-1]
         if write_addresses.shape != (B, C):

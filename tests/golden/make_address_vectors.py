@@ -1,8 +1,9 @@
 """Write tests/golden/address_vectors.json: input/output vectors of the
 reference's address producers, computed by the reference itself on the CPU.
 
-literal_addresses_from_tokens (ravel_lm/model.py:195-231) and the product-code
-decode (ProductCodeAddressor, model.py:150-187; RavelMemoryLayer._decode_codes,
+literal_addresses_from_tokens (ravel_lm/model.py:195-231), its decode-step form
+literal_addresses_step (:234-263) and the product-code decode
+(ProductCodeAddressor, model.py:150-187; RavelMemoryLayer._decode_codes,
 model.py:303-307) have no known-answer test in the reference's own suite, so
 this script imports ravel_lm.model from a reference checkout (in the build
 container only; the fixture, not the reference, travels with the tests) and
@@ -37,7 +38,7 @@ def _floats(t):
 def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from ravel_lm.model import (ProductCodeAddressor, RavelMemoryLayer,  # noqa: E402
-                                literal_addresses_from_tokens)
+                                literal_addresses_from_tokens, literal_addresses_step)
 
     g = torch.Generator().manual_seed(2024)
     literal = []
@@ -57,6 +58,26 @@ def main(ref_root: str) -> None:
         out = literal_addresses_from_tokens(toks, address_space=A, n_heads=H, bos_token_id=bos)
         literal.append({"name": name, "tokens": toks.tolist(), "address_space": A, "n_heads": H,
                         "bos_token_id": bos, "addresses": out.tolist()})
+
+    step = []
+    def ri(hi, shape):
+        return torch.randint(0, hi, shape, generator=g)
+
+    step_cases = [  # name, token ids [B], history [B, h], position, A, heads, bos
+        ("history2", ri(300, (4,)), ri(300, (4, 2)), 0, 512, 6, 257),
+        ("history2_pos", ri(300, (4,)), ri(300, (4, 2)), 777, 1000, 8, 257),
+        ("history_empty", ri(50, (3,)), torch.zeros(3, 0, dtype=torch.long), 0, 97, 4, 257),
+        ("history1", ri(50, (3,)), ri(50, (3, 1)), 3, 97, 5, 11),
+        ("history3", ri(50, (2,)), ri(50, (2, 3)), 12, 61, 7, 257),
+        ("large_position", ri(1 << 20, (2,)), ri(1 << 20, (2, 2)), (1 << 40) + 3, (1 << 31) + 11, 9, 257),
+        ("bos_history", torch.full((2,), 5), torch.full((2, 2), 257), 1, 4096, 3, 257),
+    ]
+    for name, toks, hist, pos, A, H, bos in step_cases:
+        out = literal_addresses_step(toks, hist, address_space=A, n_heads=H, position=pos,
+                                     bos_token_id=bos)
+        step.append({"name": name, "tokens": toks.tolist(), "history": hist.tolist(),
+                     "history_len": int(hist.shape[1]), "position": pos, "address_space": A,
+                     "n_heads": H, "bos_token_id": bos, "addresses": out.tolist()})
 
     codes = []
     code_cases = []
@@ -83,10 +104,12 @@ def main(ref_root: str) -> None:
                       "codebook_size": cbs, "address_space": A, "addresses": out.tolist()})
 
     doc = {
-        "source": "ravel_lm/model.py:195-231 (literal_addresses_from_tokens), "
+        "source": "ravel_lm/model.py:195-231 (literal_addresses_from_tokens), :234-263 "
+                  "(literal_addresses_step), "
                   ":150-187 + :303-307 (product-code decode), evaluated by the reference on the CPU",
         "generator": "tests/golden/make_address_vectors.py",
         "literal": literal,
+        "literal_step": step,
         "product_codes": codes,
     }
     with open(OUT, "w") as f:

@@ -215,3 +215,25 @@ def test_torch_restatement_matches_reference_outputs():
                                       codebook_size=case["codebook_size"],
                                       address_space=case["address_space"])
         assert got.tolist() == case["addresses"], case["name"]
+
+
+@pytest.mark.parametrize("case", VEC["literal_step"], ids=lambda c: c["name"])
+def test_literal_step_oracle_matches_reference_outputs(case):
+    hist = case["history"] if case["history_len"] > 0 else [[] for _ in case["tokens"]]
+    got = oa.literal_addresses_step(case["tokens"], hist, address_space=case["address_space"],
+                                    n_heads=case["n_heads"], position=case["position"],
+                                    bos_token_id=case["bos_token_id"])
+    assert got == case["addresses"]
+
+
+def test_step_equals_sequence_at_its_position():
+    """Invariant linking the two reference functions: the step at time t with
+    the previous two tokens as history gives row t of the whole sequence."""
+    case = VEC["literal"][0]
+    A, H, bos = case["address_space"], case["n_heads"], case["bos_token_id"]
+    for b, row in enumerate(case["tokens"]):
+        for t in range(len(row)):
+            hist = [[(row[t - 2] if t >= 2 else bos), (row[t - 1] if t >= 1 else bos)]]
+            got = oa.literal_addresses_step([row[t]], hist, address_space=A, n_heads=H,
+                                            position=t, bos_token_id=bos)
+            assert got[0] == case["addresses"][b][t]

@@ -231,3 +231,86 @@ def test_cfg3_shaped_lookup_from_logits(device):
     assert torch.equal(s1, s2) and torch.equal(v1, v2) and torch.equal(m1, m2)
     wm, rm = src.materialize(address_space=A)
     assert torch.equal(wm, w) and torch.equal(rm, r)
+
+
+# ------------------------------------------------------------ decode step --
+
+
+@pytest.mark.parametrize("case", VEC["literal_step"], ids=lambda c: c["name"])
+def test_literal_step_kernel_matches_reference_outputs(device, case):
+    from ravel_em import literal_addresses_step
+
+    toks = torch.tensor(case["tokens"], dtype=torch.int64, device=device)
+    B = toks.shape[0]
+    hist = torch.tensor(case["history"], dtype=torch.int64).view(B, case["history_len"]).to(device)
+    got = literal_addresses_step(toks, hist, address_space=case["address_space"],
+                                 n_heads=case["n_heads"], position=case["position"],
+                                 bos_token_id=case["bos_token_id"])
+    assert got.cpu().tolist() == case["addresses"]
+
+
+def test_chunked_prefill_with_history(device):
+    """A later chunk with the two tokens before it as history and its start as
+    position gives the addresses of the whole sequence at those times."""
+    g = torch.Generator().manual_seed(41)
+    toks = torch.randint(0, 500, (3, 200), generator=g).to(device)
+    full = literal_addresses_from_tokens(toks, address_space=1000, n_heads=7, bos_token_id=257)
+    for t0 in (1, 2, 77):
+        src = LayerAddresses(toks[:, t0:], 7, 257, token_history=toks[:, max(0, t0 - 2):t0],
+                             position=t0)
+        got, _ = src.materialize(address_space=1000)
+        assert torch.equal(got, full[:, t0:])
+
+
+def test_decode_steps_with_produced_addresses_match_the_full_lookup(device):
+    """RavelMemoryLayer's decode (model.py:401-426, history update :574) with
+    the step's addresses produced in the cache kernel, against the latest-1
+    lookup of the whole sequence with its addresses produced in the sort
+    (the reference's stepwise == full check, tests/test_model.py:78-90)."""
+    from ravel_em import RavelLayerCache
+
+    B, T, n_lit, H, Q, S, A, D, bos = 2, 40, 3, 2, 2, 8, 97, 8, 257
+    g = torch.Generator().manual_seed(43)
+    toks = torch.randint(0, 60, (B, T), generator=g).to(device)
+    packed = torch.randn(B, T, 2 * H * Q * S, generator=g).to(torch.bfloat16).to(device)
+    wl, rl = packed[..., :H * Q * S], packed[..., H * Q * S:]
+    payload = torch.randn(B, T, n_lit + H, D, generator=g).to(device)
+    src = LayerAddresses(toks, n_lit, bos, wl, rl, H, Q, S)
+    full_v, full_m = causal_last_k_lookup(src, payload, address_space=A, k=1)
+    cache = RavelLayerCache.empty(B, n_lit + H, A, D, device=device, dtype=payload.dtype)
+    hist = torch.full((B, 2), bos, dtype=torch.long, device=device)
+    for t in range(T):
+        step = LayerAddresses(toks[:, t], n_lit, bos, wl[:, t], rl[:, t], H, Q, S,
+                              token_history=hist, position=t)
+        v, m = cache.step(step, None, payload[:, t])
+        assert torch.equal(m, full_m[:, t, :, 0]), t
+        assert torch.equal(v, full_v[:, t, :, 0]), t
+        hist = torch.cat([hist[:, 1:], toks[:, t:t + 1]], dim=1)
+
+
+@pytest.mark.parametrize("k", [1, 4])
+def test_cache_step_with_produced_addresses_matches_tensor_step(device, k):
+    from ravel_em import RavelLayerCache, literal_addresses_step, product_code_addresses
+
+    B, n_lit, H, Q, S, A, D, bos = 8, 2, 3, 2, 16, 300, 16, 257
+    C = n_lit + H
+    g = torch.Generator().manual_seed(47 + k)
+    c1 = RavelLayerCache.empty(B, C, A, D, device=device, dtype=torch.bfloat16, k=k)
+    c2 = RavelLayerCache.empty(B, C, A, D, device=device, dtype=torch.bfloat16, k=k)
+    hist = torch.randint(0, 300, (B, 2), generator=g).to(device)
+    for t in range(12):
+        tok = torch.randint(0, 300, (B,), generator=g).to(device)
+        wl = torch.randn(B, H * Q * S, generator=g).to(torch.bfloat16).to(device)
+        rl = torch.randn(B, H * Q * S, generator=g).to(torch.bfloat16).to(device)
+        pay = torch.randn(B, C, D, generator=g).to(torch.bfloat16).to(device)
+        lit = literal_addresses_step(tok, hist, address_space=A, n_heads=n_lit, position=t + 5,
+                                     bos_token_id=bos)
+        kw = dict(n_heads=H, n_codebooks=Q, codebook_size=S, address_space=A)
+        w = torch.cat([lit, product_code_addresses(wl, **kw)], dim=-1)
+        r = torch.cat([lit, product_code_addresses(rl, **kw)], dim=-1)
+        v2, m2 = c2.step(r, w, pay)
+        src = LayerAddresses(tok, n_lit, bos, wl, rl, H, Q, S, token_history=hist, position=t + 5)
+        v1, m1 = c1.step(src, None, pay)
+        assert torch.equal(m1, m2) and torch.equal(v1, v2), t
+        hist = torch.cat([hist[:, 1:], tok.view(-1, 1)], dim=1)
+    assert torch.equal(c1.values, c2.values) and torch.equal(c1.filled, c2.filled)
