@@ -206,9 +206,85 @@ def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
     us = statistics.median(t) / steps
     lines.append(_line("cfg5", "decode_step_graph", us, step_bytes, B, steps=steps,
                        steps_per_s=1e6 / us, graph_steps=graph_chunk))
+    lines += decode_address_lines(dev, cache, w)
     if cpu is not None:
         for line in lines:
-            line["cpu_baseline"] = cpu(w, line["op"])
+            if "from_tokens" not in line["op"]:
+                line["cpu_baseline"] = cpu(w, line["op"])
+    return lines
+
+
+def decode_address_lines(dev: torch.device, cache: RavelLayerCache, w, steps: int = 256,
+                         graph_chunk: int = 128) -> List[dict]:
+    """The cfg5 cache stepped by a memory layer whose 8 heads are the literal
+    families of the step's token (ravel_lm/model.py:401-426, history update
+    :574): the reference's address ops as torch ops then the cache step
+    ("chain"), against the cache step producing its addresses itself
+    ("fused"); eager and replayed from HIP graphs."""
+    from .addressing import LayerAddresses
+
+    B, H = w.step_read.shape[1:]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1016)
+    toks = workloads.zipf((steps, B), w.address_space, g)
+    hist0 = workloads.zipf((B, 2), w.address_space, g)
+    A, bos = w.address_space, workloads.BOS
+    hist = hist0.clone()
+
+    def chain_step(s):
+        a = workloads.literal_addresses_step(toks[s], hist, address_space=A, n_heads=H, position=s)
+        out = cache.step(a, a, w.step_payload[s])
+        hist.copy_(torch.cat([hist[:, 1:], toks[s].view(-1, 1)], dim=1))
+        return out
+
+    def fused_step(s):
+        src = LayerAddresses(toks[s], H, bos, token_history=hist, position=s)
+        out = cache.step(src, None, w.step_payload[s])
+        hist.copy_(torch.cat([hist[:, 1:], toks[s].view(-1, 1)], dim=1))
+        return out
+
+    # both forms read the same values on the same cache state (first steps,
+    # from a saved copy of the cache)
+    saved = (cache.values.clone(), cache.filled.clone())
+    hist.copy_(hist0)
+    ref = [chain_step(s)[0].clone() for s in range(4)]
+    cache.values.copy_(saved[0])
+    cache.filled.copy_(saved[1])
+    hist.copy_(hist0)
+    same = all(torch.equal(fused_step(s)[0], ref[s]) for s in range(4))
+    del saved
+    lines = []
+    for form, fn in (("chain", chain_step), ("fused", fused_step)):
+        def eager():
+            hist.copy_(hist0)
+            for s in range(steps):
+                fn(s)
+        t = time_calls(eager, warmup=1, iters=3)
+        us = statistics.median(t) / steps
+        lines.append(_line("cfg5", f"decode_step_from_tokens_{form}_eager", us, 0, B,
+                           steps=steps, steps_per_s=1e6 / us, heads=int(H), same_reads=same))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for s in range(3):
+                fn(s)
+        torch.cuda.current_stream().wait_stream(side)
+        graphs = []
+        for c0 in range(0, steps, graph_chunk):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for s in range(c0, min(steps, c0 + graph_chunk)):
+                    fn(s)
+            graphs.append(gr)
+
+        def replay():
+            hist.copy_(hist0)
+            for gr in graphs:
+                gr.replay()
+        t = time_calls(replay, warmup=1, iters=5)
+        us = statistics.median(t) / steps
+        lines.append(_line("cfg5", f"decode_step_from_tokens_{form}_graph", us, 0, B,
+                           steps=steps, steps_per_s=1e6 / us, graph_steps=graph_chunk, heads=int(H)))
     return lines
 
 

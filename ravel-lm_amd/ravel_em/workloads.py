@@ -81,6 +81,29 @@ def literal_addresses(tokens: Tensor, *, address_space: int, n_heads: int, bos: 
     return torch.stack(heads, dim=-1)
 
 
+def literal_addresses_step(tokens: Tensor, history: Tensor, *, address_space: int, n_heads: int,
+                           position: int, bos: int = BOS) -> Tensor:
+    """One decode step of the literal families (ravel_lm/model.py:234-263):
+    tokens [B], history [B, 2] = [prev2, prev1]; torch ops on the device, the
+    reference's own formulation (timed against the in-kernel production)."""
+    toks = tokens.long()
+    A = address_space
+    prev1 = history[:, -1].long() if history.numel() else torch.full_like(toks, bos)
+    prev2 = history[:, -2].long() if history.shape[1] >= 2 else torch.full_like(toks, bos)
+    heads = []
+    for j in range(n_heads):
+        if j == 0:
+            h = toks
+        elif j == 1:
+            h = prev1 * 257 + toks * 131 + 17
+        elif j == 2:
+            h = prev2 * 65537 + prev1 * 257 + toks * 131 + 31
+        else:
+            h = toks * (1009 + 2 * j) + int(position) * (9176 + j) + j * 97
+        heads.append(h.remainder(A))
+    return torch.stack(heads, dim=-1)
+
+
 def zipf(shape, n: int, g: torch.Generator, s: float = 1.1) -> Tensor:
     """Draws from p(r) proportional to r^-s over ranks r = 1..n; returns r-1."""
     ranks = torch.arange(1, n + 1, device=g.device, dtype=torch.float64)
