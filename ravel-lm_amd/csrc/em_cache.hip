@@ -240,6 +240,57 @@ __global__ __launch_bounds__(256) void prefill_tail_kernel(const U* __restrict__
   }
 }
 
+// Prefill, kept records: after the cache is zero-filled (at the write rate),
+// one block per segment stages the segment's sorted keys in LDS; the record at
+// sorted position p goes to slot e = the number of later records of its
+// address (counted in LDS, capped at k) when e < k.  Only kept rows are read
+// and written, and no thread waits on a chain of global key loads.
+constexpr int kPrefillLds = 32 * 1024;  // sorted keys of one segment
+constexpr int kPrefillBatch = 4;        // kept rows in flight per thread
+
+template <typename U, typename V>
+__global__ __launch_bounds__(256) void prefill_kept_kernel(
+    const U* __restrict__ sorted, const V* __restrict__ payload, int64_t T, int64_t C, int64_t A,
+    int tbits, int64_t k, int64_t upr, V* __restrict__ values, uint8_t* __restrict__ filled) {
+  extern __shared__ __align__(16) unsigned char prefill_lds[];
+  U* keys = (U*)prefill_lds;
+  const int Ti = (int)T;
+  const int64_t seg = blockIdx.x;
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const U* sk = sorted + seg * T;
+  for (int i = threadIdx.x; i < Ti; i += 256) keys[i] = sk[i];
+  __syncthreads();
+  const U tmask = (U)((((uint64_t)1) << tbits) - 1);
+  const int64_t units = T * upr;
+  for (int64_t g0 = threadIdx.x; g0 < units; g0 += 256 * kPrefillBatch) {
+    V val[kPrefillBatch];
+    int64_t dst[kPrefillBatch];
+#pragma unroll
+    for (int j = 0; j < kPrefillBatch; ++j) {  // every kept row's load first
+      const int64_t g = g0 + j * 256;
+      dst[j] = -1;
+      if (g >= units) continue;
+      const int p = (int)(g / upr);
+      const int64_t v = g - (int64_t)p * upr;
+      const U u = keys[p];
+      const U a = u >> tbits;
+      if ((int64_t)a >= A) continue;  // masked record (sorted last)
+      int64_t e = 0;  // later records of the same address, capped at k
+      while (e < k && p + 1 + e < Ti && (keys[p + 1 + e] >> tbits) == a) ++e;
+      if (e >= k) continue;
+      const int64_t t = (int64_t)(u & tmask);
+      dst[j] = ((seg * A + (int64_t)a) * k + e) * upr + v;
+      val[j] = payload[((b * T + t) * C + c) * upr + v];
+    }
+#pragma unroll
+    for (int j = 0; j < kPrefillBatch; ++j) {
+      if (dst[j] < 0) continue;
+      values[dst[j]] = val[j];
+      if (dst[j] % upr == 0) filled[dst[j] / upr] = 1;
+    }
+  }
+}
+
 template <typename V>
 hipError_t cache_read_t(const void* values, const uint8_t* filled, const void* addr, bool addr64,
                         int64_t BC, int64_t A, int64_t k, int64_t upr, void* out, uint8_t* omask,
@@ -346,6 +397,21 @@ hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, i
   if (N == 0) return hipSuccess;
   const int vb = vec_bytes((uintptr_t)values | (uintptr_t)payload | (uintptr_t)row_bytes);
   const int64_t upr = row_bytes / vb;
+  const size_t kept_lds = (size_t)tp.T * sizeof(U);
+  if (kept_lds <= (size_t)kPrefillLds) {
+#define REM_PREFILL(VT)                                                                          \
+  prefill_kept_kernel<U, VT><<<(unsigned)BC, 256, kept_lds, s>>>(                                \
+      sorted, (const VT*)payload, tp.T, tp.C, tp.A, tp.tbits, k, upr, (VT*)values, filled)
+    switch (vb) {
+      case 16: REM_PREFILL(u32x4); break;
+      case 8: REM_PREFILL(u32x2); break;
+      case 4: REM_PREFILL(uint32_t); break;
+      case 2: REM_PREFILL(uint16_t); break;
+      default: REM_PREFILL(uint8_t); break;
+    }
+#undef REM_PREFILL
+    return hipGetLastError();
+  }
   const unsigned grid = grid_for(N * upr, 256);
 #define REM_PREFILL(VT)                                                                          \
   prefill_tail_kernel<U, VT><<<grid, 256, 0, s>>>(sorted, (const VT*)payload, N, tp.T, tp.C,     \

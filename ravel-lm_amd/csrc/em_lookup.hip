@@ -609,11 +609,19 @@ __global__ __launch_bounds__(kRowsThreads) void link_rows_lds_kernel(const U* __
   }
 }
 
-__global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n,
-                                                     uint8_t v) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = v;
+// Fill of n bytes: the 16-byte-aligned body with 16-byte stores (measured at
+// torch's fill rate, 6.8 TB/s on 4.3 GB; non-temporal stores were slower), the
+// unaligned head and tail byte by byte.
+__global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ p, int64_t n,
+                                                   int64_t head, int64_t body, uint8_t v) {
+  const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint32_t w = 0x01010101u * v;
+  const u32x4 vv = {w, w, w, w};
+  u32x4* q = (u32x4*)(p + head);
+  for (int64_t i = tid; i < body; i += stride) q[i] = vv;
+  const int64_t rest = n - body * 16;  // head + tail bytes
+  for (int64_t i = tid; i < rest; i += stride) p[i < head ? i : i + body * 16] = v;
 }
 
 }  // namespace
@@ -632,8 +640,12 @@ int dtype_size(int dtype) {
 
 hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
-  fill_u8_kernel<<<grid_for((int64_t)bytes, 256), 256, 0, s>>>((uint8_t*)dst, (int64_t)bytes,
-                                                               value);
+  const int64_t n = (int64_t)bytes;
+  int64_t head = (int64_t)((16 - ((uintptr_t)dst & 15)) & 15);
+  if (head > n) head = n;
+  const int64_t body = (n - head) / 16;
+  fill_kernel<<<grid_for(body > 0 ? body : 1, 256), 256, 0, s>>>((uint8_t*)dst, n, head, body,
+                                                                  value);
   return hipGetLastError();
 }
 

@@ -82,12 +82,18 @@ def test_step_equals_read_then_write(device, k):
     assert torch.equal(c1.values, c2.values) and torch.equal(c1.filled, c2.filled)
 
 
-@pytest.mark.parametrize("k,masked", [(1, False), (4, False), (3, True)])
-def test_prefill_matches_sequential_writes(device, k, masked):
+# A <= 8000 and short segments take the one-pass region writer (the segment's
+# keys and per-address run bounds in LDS); A = 20000 the fill-then-scatter
+# path.  D = 3 fp32 rows are 12 bytes (4-byte units).
+@pytest.mark.parametrize("k,masked,A,D,dtype", [
+    (1, False, 37, 8, torch.bfloat16), (4, False, 37, 8, torch.bfloat16),
+    (3, True, 37, 8, torch.bfloat16), (2, True, 4099, 3, torch.float32),
+    (4, False, 20000, 8, torch.bfloat16)])
+def test_prefill_matches_sequential_writes(device, k, masked, A, D, dtype):
     g = torch.Generator().manual_seed(20 + k)
-    B, T, C, A, D = 3, 500, 4, 37, 8
+    B, T, C = 3, 500, 4
     w = torch.randint(-5, A + 5, (B, T, C), generator=g)
-    p = torch.randn(B, T, C, D, generator=g).to(torch.bfloat16)
+    p = torch.randn(B, T, C, D, generator=g).to(dtype)
     m = (torch.rand(B, T, generator=g) < 0.7) if masked else None
     cache = RavelLayerCache.prefill(w.to(device), p.to(device), address_space=A, k=k,
                                     write_mask=None if m is None else m.to(device))
