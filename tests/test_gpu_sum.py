@@ -5,11 +5,14 @@ accurate, so the ground truth is fp64 per-stream sums):
   fp32 / fp64 payloads: |gpu - truth| <= 1e-5 |truth| + 1e-7 * sum|x|
   bf16 / fp16 payloads: |gpu - truth| <= 1e-2 |truth| + 1e-4 * sum|x|
 where sum|x| is the per-output sum of absolute payload values (the scale of the
-accumulation).  Masks are exact.
+accumulation).  Masks are exact.  The reference's own outputs on small inputs
+(tests/golden/sum_vectors.json) are matched bit-exactly where its arithmetic is
+exact and within its rounding bound elsewhere.
 """
 import pytest
 import torch
 
+import golden_sums
 import oracle
 from ravel_em import causal_sum_lookup, workloads
 
@@ -94,3 +97,24 @@ def test_sum_baseline_configs(device, name):
         "cfg4_adv": lambda: workloads.cfg4(device, adversarial=True, B=1),
     }[name]()
     check_sum(w.write, w.payload, w.read, A=w.address_space)
+
+
+@pytest.mark.parametrize("case", golden_sums.CASES, ids=lambda c: c["name"])
+def test_sum_matches_reference_outputs(device, case):
+    """The reference's own outputs (tests/golden/sum_vectors.json): masks bit-exact;
+    integer cases, exact in the reference's arithmetic, bit-exact; otherwise
+    |gpu - reference| <= (the reference's rounding bound) + (this kernel's tolerance
+    against the exact sum above)."""
+    w, r, p, A, m, ref, rmask = golden_sums.tensors(case)
+    out, omask = causal_sum_lookup(w.to(device), p.to(device), None if r is None else r.to(device),
+                                   address_space=A, write_mask=None if m is None else m.to(device))
+    out, omask = out.cpu(), omask.cpu()
+    assert out.dtype == ref.dtype and torch.equal(omask, rmask)
+    if case["name"].startswith("int_") or case["name"] in ("all_masked", "single_address"):
+        assert torch.equal(out, ref)
+        return
+    truth, _ = oracle.seg_sum(w, p, r, address_space=A, write_mask=m)
+    scale, _ = oracle.seg_sum(w, p.abs(), r, address_space=A, write_mask=m)
+    rtol, atol = TOL[p.dtype]
+    lim = golden_sums.reference_bound(p, truth, m) + rtol * truth.abs() + atol * scale
+    assert ((out.double() - ref.double()).abs() <= lim).all()
