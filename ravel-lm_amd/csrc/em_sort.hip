@@ -242,6 +242,11 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
 // Fused path.  pack_hist -> seg_offsets or scan_hist -> scatter0 (pass 0,
 // reduce-then-scan) -> sweep (passes >= 1, decoupled look-back).  Used when the per-block LDS
 // budget below holds; the generic path above handles every other shape.
+// The read == write, k == 1 link of 32-bit keys rides on the last pass
+// (sweep_link_kernel).  With exactly two digit passes and short segments each
+// segment chooses on the device: scatter by the high digit and link inside its
+// buckets (bucket_link_kernel), or, when a bucket is too large for one block,
+// scatter by the low digit and link in the look-back sweep.
 
 constexpr int kPackThreads = 512;
 constexpr int kPackLdsBytes = 33 * 1024;  // keys of one pack tile, [CC][TT + 1]
@@ -267,13 +272,14 @@ __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t wor
 
 // One block packs TT time steps of CC heads of one batch row: the [TT, CC]
 // slab of the [B,T,C] address tensor goes through LDS into segment-major keys,
-// with per-(segment, tile) histograms of every digit pass.  Sibling head
+// with per-(segment, tile) histograms of the digit passes [h0, h0 + nh) (the
+// passes whose scatter needs offsets).  Sibling head
 // groups of one time tile are consecutive logical blocks, which xcd_block
 // places on one XCD, so the 128-byte address rows they share stay in one L2.
 template <typename U, typename AS>
 __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
-    int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int npass, int ntiles,
+    int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int h0, int nh, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
     uint32_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
   __shared__ U tile[kPackLdsBytes / sizeof(U)];
@@ -291,7 +297,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
   const int tt = (int)((T - t0) < TT ? (T - t0) : TT);
   const int n = tt * cc;
   const int pitch = TT + 1;
-  const int per = npass * kRadix;
+  const int per = nh * kRadix;
+  const int hshift = tbits + 8 * h0;
   const int hw = cc * per;
   for (int i = threadIdx.x; i < hw; i += kPackThreads) h[i] = 0;
   __syncthreads();
@@ -313,8 +320,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
         if (wmask && !wmask[b * T + t0 + tl]) a = A;
         const U u = ((U)a << tbits) | (U)(t0 + tl);
         tile[cl * pitch + tl] = u;
-        for (int p = 0; p < npass; ++p)
-          atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (tbits + 8 * p)) & (kRadix - 1))], 1u);
+        for (int p = 0; p < nh; ++p)
+          atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (hshift + 8 * p)) & (kRadix - 1))], 1u);
       }
     }
   }
@@ -324,7 +331,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const int tl = i - cl * tt;
     keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
   }
-  // hist layout [seg][tile][pass][256]: one contiguous npass KB run per head.
+  // hist layout [seg][tile][pass][256]: one contiguous nh KB run per head.
   for (int i = threadIdx.x; i < hw; i += kPackThreads) {
     const int cl = i / per;
     const int r = i - cl * per;
@@ -336,7 +343,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
 // scatter tile (m consecutive pack tiles): offs[seg][tile][d] = count of digit d
 // in the segment's earlier scatter tiles.  Also resets the look-back tickets.
 __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restrict__ hist,
-                                                        int ntiles, int m, int npass,
+                                                        int ntiles, int m, int nh, int npass,
                                                         uint32_t* __restrict__ offs, int nsct,
                                                         uint32_t* __restrict__ binbase,
                                                         uint32_t* __restrict__ tickets) {
@@ -347,7 +354,7 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restr
   const int d = threadIdx.x % kRadix;
   const int g = threadIdx.x / kRadix;
   const int64_t seg = blockIdx.x;
-  const int per = npass * kRadix;
+  const int per = nh * kRadix;
   const uint32_t* hs = hist + seg * (int64_t)ntiles * per;
   // group g owns whole scatter tiles [slo, shi), i.e. pack tiles [slo*m, shi*m)
   const int slen = (nsct + G - 1) / G;
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restr
   const int hi = (shi * m) < ntiles ? (shi * m) : ntiles;
   if (threadIdx.x < npass) tickets[(int64_t)threadIdx.x * gridDim.x + seg] = 0;  // [pass][seg]
   if (seg == 0 && threadIdx.x == 0) tickets[(int64_t)npass * gridDim.x] = 0;   // error word
-  for (int p = 0; p < npass; ++p) {
+  for (int p = 0; p < nh; ++p) {
     uint32_t sum = 0;
     for (int t0 = lo; t0 < hi; t0 += U8) {
       uint32_t v[U8];
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restr
     // Every thread takes part in the block scan (it synchronizes); only group
     // 0 contributes, so thread d of group 0 receives the sum over digits < d.
     const uint32_t ex = block_excl_scan<1024>(g == 0 ? total : 0u, tmp, nullptr);
-    if (g == 0) binbase[(seg * npass + p) * kRadix + d] = ex;
+    if (g == 0) binbase[(seg * nh + p) * kRadix + d] = ex;
     __syncthreads();
   }
 }
@@ -485,20 +492,28 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
 }
 
 // Pass offsets of a segment with at most kShortMaxTiles pack tiles: one block
-// per (segment, pass), thread d = digit.  binbase[seg][pass][d] = exclusive
-// scan over digits of the segment's digit totals; for pass 0 also
-// offs[seg][scatter tile][d] = count of digit d in the earlier scatter tiles
-// (2^lm pack tiles each).  Resets the look-back tickets and the error word.
+// per (segment, histogram pass), thread d = digit.  binbase[seg][pass][d] =
+// exclusive scan over digits of the segment's digit totals; for the first
+// noffs histogram passes (the candidates for the first scatter) also
+// offs[pass][seg][scatter tile][d] = count of digit d in the earlier scatter
+// tiles (2^lm pack tiles each).  With `modes`, the block of histogram pass 1
+// (the high digit of a two-pass key) sets modes[seg] = 1 when no bucket of
+// that digit holds more than bucket_max keys (the segment then scatters by the
+// high digit and links by buckets), else 0 (low digit first, look-back link).
+// Resets the look-back tickets of all npass passes and the error word.
 constexpr int kShortMaxTiles = 64;
 
 __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
-    const uint32_t* __restrict__ hist, int nt0, int lm, int npass, uint32_t* __restrict__ offs,
-    int nsct, uint32_t* __restrict__ binbase, uint32_t* __restrict__ tickets, int64_t nseg) {
+    const uint32_t* __restrict__ hist, int nt0, int lm, int nh, int npass,
+    uint32_t* __restrict__ offs, int nsct, uint32_t* __restrict__ binbase,
+    uint32_t* __restrict__ tickets, int64_t nseg, int noffs, uint32_t* __restrict__ modes,
+    uint32_t bucket_max) {
   __shared__ uint32_t tmp[kSortThreads / kWave + 1];
+  __shared__ uint32_t s_big;
   const int d = threadIdx.x;
-  const int64_t seg = blockIdx.x / npass;
-  const int p = (int)(blockIdx.x - seg * npass);
-  const int per = npass * kRadix;
+  const int64_t seg = blockIdx.x / nh;
+  const int p = (int)(blockIdx.x - seg * nh);
+  const int per = nh * kRadix;
   const uint32_t* hs = hist + seg * (int64_t)nt0 * per + p * kRadix + d;
   uint32_t v[kShortMaxTiles];
 #pragma unroll
@@ -506,17 +521,24 @@ __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
   uint32_t tot = 0;
 #pragma unroll
   for (int j = 0; j < kShortMaxTiles; ++j) tot += v[j];
-  binbase[(seg * npass + p) * kRadix + d] = block_excl_scan<kSortThreads>(tot, tmp, nullptr);
-  if (p == 0) {
+  if (modes && p == 1 && d == 0) s_big = 0;
+  binbase[(seg * nh + p) * kRadix + d] = block_excl_scan<kSortThreads>(tot, tmp, nullptr);
+  if (p < noffs) {
     const int mmask = (1 << lm) - 1;
+    uint32_t* op = offs + (int64_t)p * nseg * nsct * kRadix;
     uint32_t run = 0;
 #pragma unroll
     for (int j = 0; j < kShortMaxTiles; ++j) {
-      if (j < nt0 && (j & mmask) == 0) offs[(seg * nsct + (j >> lm)) * kRadix + d] = run;
+      if (j < nt0 && (j & mmask) == 0) op[(seg * nsct + (j >> lm)) * kRadix + d] = run;
       run += v[j];
     }
   }
-  if (d == 0) tickets[(int64_t)p * nseg + seg] = 0;  // [pass][seg]
+  if (modes && p == 1) {  // s_big was set before the scan's barriers
+    if (tot > bucket_max) s_big = 1;
+    __syncthreads();
+    if (d == 0) modes[seg] = s_big ? 0u : 1u;
+  }
+  if (p == 0 && d < npass) tickets[(int64_t)d * nseg + seg] = 0;  // [pass][seg]
   if (blockIdx.x == 0 && d == 0) tickets[(int64_t)npass * nseg] = 0;  // error word
 }
 
@@ -524,7 +546,8 @@ template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
     const uint32_t* __restrict__ binbase, int npass, int64_t T, int ntiles, int64_t nblk,
-    int shift, uint32_t* __restrict__ zero0, int64_t zero0_words) {
+    int shift, uint32_t* __restrict__ zero0, int64_t zero0_words,
+    const uint32_t* __restrict__ modes, int64_t offs_pass_words) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
@@ -541,10 +564,13 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   const int tile = (int)(lb - seg * ntiles);
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  // modes[seg] = 1: this segment scatters by histogram pass 1 (the next digit)
+  const int mp = modes ? (int)modes[seg] : 0;
+  shift += 8 * mp;
   U key[ITEMS];
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
-  const int64_t gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
-                       (int64_t)binbase[seg * npass * kRadix + tid];
+  const int64_t gofs = (int64_t)offs[mp * offs_pass_words + (seg * ntiles + tile) * (int64_t)kRadix + tid] +
+                       (int64_t)binbase[(seg * npass + mp) * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
   rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
@@ -653,7 +679,8 @@ template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
     const uint32_t* __restrict__ in, uint64_t* __restrict__ status,
     uint32_t* __restrict__ ticket, int64_t T, int64_t C, int ntiles, int64_t nblk, int shift,
-    int tbits, uint32_t* __restrict__ err, int32_t* __restrict__ src_seg) {
+    int tbits, uint32_t* __restrict__ err, int32_t* __restrict__ src_seg,
+    const uint32_t* __restrict__ modes) {
   using U = uint32_t;
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
@@ -668,6 +695,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   if (lb >= nblk) return;  // uniform per block
   const int64_t seg = lb / ntiles;
+  if (modes && modes[seg]) return;  // uniform per block: this segment links by buckets
   if (tid == 0) s_ticket = atomicAdd(&ticket[seg], 1u);
   __syncthreads();
   const int tile = (int)s_ticket;
@@ -758,6 +786,171 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
   }
 }
 
+// Read == write, k == 1, 32-bit keys, two digit passes: the link without a
+// second global pass.  The only scatter went by the HIGH digit, so each
+// segment's keys sit in buckets of one high digit, in time order inside a
+// bucket (the scatter is stable).  Two records share an address iff they share
+// the bucket and the low digit, so a record's same-address predecessor is the
+// previous key of its bucket with the same low digit.
+//
+// A wave walks a run of its bucket 64 keys at a time, in order:
+//   peers = lanes of this step with the same low digit: one ballot for the
+//           lanes sharing lane 0's digit, and for the other lanes a per-wave
+//           table of 256 lane masks in LDS (OR the lane bit in, read the word,
+//           clear it), so a digit that fills most of a step costs one ballot,
+//           not a queue of same-address LDS atomics;
+//   predecessor = the highest peer below the lane (its time by ds_bpermute),
+//           else the wave's last time of that digit from earlier steps of the
+//           run (a per-wave table of 256 words), which the digit's highest
+//           lane then replaces with its own time.
+// A wave's LDS operations execute in issue order, so every read sees exactly
+// the writes of earlier steps and of this step's earlier instructions.
+//
+// The block of logical id (seg, g) owns buckets 16g..16g+15 of segment seg.
+// A bucket of at most kLinkRun keys is one run of one wave (wave w takes
+// bucket 16g + w; uniform addresses put ~T/256 keys in a bucket).  A larger
+// bucket is walked by all 16 waves of the block together, in rounds of 16
+// runs: after a round a block barrier, then per digit the last time before
+// each wave's run (from earlier waves' tables and a running carry over the
+// rounds), then each wave resolves the keys of its run that had no
+// predecessor inside the run.  No look-back, no wait on another block.
+constexpr int kLinkWaves = 16;
+constexpr int kLinkThreads = kLinkWaves * kWave;
+constexpr int kLinkSteps = 16;
+constexpr int kLinkRun = kLinkSteps * kWave;  // keys of one wave's run
+constexpr uint32_t kLHas32 = 1u << 31;        // table word: has a key | its time
+
+template <bool COOP>
+__device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, int64_t start,
+                                             int64_t end, int tbits, uint64_t* mt, uint32_t* lt,
+                                             int32_t vbase, int32_t Ci, int32_t* __restrict__ dst,
+                                             uint32_t* u) {
+  const int lane = threadIdx.x % kWave;
+  const uint32_t tmask = (1u << tbits) - 1u;
+  const uint64_t bit = 1ull << lane;
+  const uint64_t below_mask = bit - 1ull;
+  const uint64_t above_mask = ~(below_mask | bit);
+#pragma unroll
+  for (int i = 0; i < kRadix / kWave; ++i) lt[i * kWave + lane] = 0;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int st = 0; st < kLinkSteps; ++st) {
+    const int64_t idx = start + st * kWave + lane;
+    u[st] = idx < end ? kk[idx] : 0u;
+  }
+  uint32_t first = 0;  // steps whose key had no predecessor inside the run
+#pragma unroll
+  for (int st = 0; st < kLinkSteps; ++st) {
+    if (start + st * kWave >= end) break;  // uniform
+    const bool valid = start + st * kWave + lane < end;
+    const uint32_t d = (u[st] >> tbits) & (kRadix - 1);
+    const uint32_t tm = u[st] & tmask;
+    // lane 0 is valid in every step that runs
+    const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
+    const bool rest = valid && d != d0;
+    const uint64_t eq0 = __ballot(valid && d == d0);
+    if (rest) atomicOr((unsigned long long*)&mt[d], (unsigned long long)bit);
+    __builtin_amdgcn_wave_barrier();
+    uint64_t peers = eq0;
+    if (rest) peers = mt[d];
+    const uint32_t carry = valid ? lt[d] : 0u;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (peers & above_mask) == 0) {  // the digit's highest lane in this step
+      if (rest) mt[d] = 0;
+      lt[d] = kLHas32 | tm;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t lower = peers & below_mask;
+    const int jl = lower ? 63 - __builtin_clzll(lower) : lane;
+    const uint32_t pt = (uint32_t)__shfl((int)tm, jl, kWave);
+    if (valid) {
+      if (lower)
+        dst[tm] = vbase + (int32_t)pt * Ci;
+      else if (carry)
+        dst[tm] = vbase + (int32_t)(carry & ~kLHas32) * Ci;
+      else if (!COOP)
+        dst[tm] = -1;
+      else
+        first |= 1u << st;
+    }
+  }
+  return first;
+}
+
+__global__ __launch_bounds__(kLinkThreads) void bucket_link_kernel(
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ binbase, int64_t T,
+    int64_t C, int tbits, int nbuck, int ngrp, int64_t nlogical, int32_t* __restrict__ src_seg,
+    const uint32_t* __restrict__ modes) {
+  __shared__ __align__(16) uint64_t mtab[kLinkWaves][kRadix];  // all zero between steps
+  __shared__ __align__(16) uint32_t ltab[kLinkWaves][kRadix];  // kLHas32 | time, 0 = none
+  __shared__ __align__(16) uint32_t ctab[kLinkWaves][kRadix];  // carry into a wave's run
+  __shared__ uint32_t runc[kRadix];  // carry after the rounds so far
+  __shared__ uint32_t bstart[kLinkWaves + 1];
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
+  if (logical >= nlogical) return;  // uniform per block
+  const int64_t seg = logical / ngrp;
+  if (!modes[seg]) return;  // uniform per block: this segment links by look-back
+  const int b0 = (int)(logical - seg * ngrp) * kLinkWaves;
+  const uint32_t* bb = binbase + (seg * 2 + 1) * kRadix;  // the high digit's bucket starts
+  if (tid <= kLinkWaves) {
+    const int x = b0 + tid;
+    bstart[tid] = x < nbuck ? bb[x] : (x < kRadix ? bb[x] : (uint32_t)T);
+  }
+  uint64_t* mt = mtab[w];
+  uint32_t* lt = ltab[w];
+#pragma unroll
+  for (int i = 0; i < kRadix / kWave; ++i) mt[i * kWave + lane] = 0;
+  __syncthreads();
+  const uint32_t* kk = keys + seg * T;
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  int32_t* dst = src_seg + seg * T;
+  const uint32_t tmask = (1u << tbits) - 1u;
+  uint32_t u[kLinkSteps];
+  // Small buckets: one wave each.
+  {
+    const int64_t lo = bstart[w], hi = bstart[w + 1];
+    if (b0 + w < nbuck && hi - lo <= kLinkRun)
+      link_run<false>(kk, lo, hi, tbits, mt, lt, vbase, Ci, dst, u);
+  }
+  // Large buckets: the block's waves together (block-uniform loop).
+  for (int x = 0; x < kLinkWaves; ++x) {
+    const int64_t lo = bstart[x], hi = bstart[x + 1];
+    if (b0 + x >= nbuck || hi - lo <= kLinkRun) continue;
+    for (int64_t r0 = lo; r0 < hi; r0 += (int64_t)kLinkWaves * kLinkRun) {
+      const int64_t s0 = r0 + (int64_t)w * kLinkRun;
+      const int64_t e0 = (s0 + kLinkRun) < hi ? (s0 + kLinkRun) : hi;
+      uint32_t first = 0;
+      if (s0 < e0) {
+        first = link_run<true>(kk, s0, e0, tbits, mt, lt, vbase, Ci, dst, u);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kRadix / kWave; ++i) lt[i * kWave + lane] = 0;
+      }
+      __syncthreads();  // every wave's last times
+      if (tid < kRadix) {
+        uint32_t cy = r0 == lo ? 0u : runc[tid];
+#pragma unroll
+        for (int v = 0; v < kLinkWaves; ++v) {
+          ctab[v][tid] = cy;
+          const uint32_t l = ltab[v][tid];
+          if (l) cy = l;
+        }
+        runc[tid] = cy;
+      }
+      __syncthreads();  // every wave's carries
+#pragma unroll
+      for (int st = 0; st < kLinkSteps; ++st) {
+        if ((first >> st) & 1u) {
+          const uint32_t cy = ctab[w][(u[st] >> tbits) & (kRadix - 1)];
+          dst[u[st] & tmask] = cy ? vbase + (int32_t)(cy & ~kLHas32) * Ci : -1;
+        }
+      }
+    }
+  }
+}
+
 int pack_tt(int64_t C, size_t key_bytes) {
   int tt = kPackTT;
   while (tt > 1 && (size_t)C * (size_t)(tt + 1) * key_bytes > 48 * 1024) tt >>= 1;
@@ -811,6 +1004,12 @@ int64_t scatter0_tiles(const Tape& tp) {
   return (tp.T + kT - 1) / kT;
 }
 
+// Two 8-bit digits, 32-bit keys, short segments (seg_offsets_kernel): the
+// link may go by buckets of the high digit.
+bool bucket_mode(const Tape& tp, size_t key_bytes, int64_t nt0) {
+  return key_bytes == 4 && (tp.abits + 7) / 8 == 2 && nt0 <= kShortMaxTiles;
+}
+
 size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
   const int tt = fused_plan(tp, key_bytes).TT;
   if (!tt) return 0;
@@ -820,8 +1019,10 @@ size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
   const int64_t offs = tp.nseg() * scatter0_tiles(tp) * kRadix;
   const int64_t bins = tp.nseg() * npass * kRadix;
   const int64_t status = tp.nseg() * sweep_tiles(tp) * kRadix;
+  // bucket mode: offsets of two candidate first digits and the segment modes
+  const int64_t bucket = bucket_mode(tp, key_bytes, nt0) ? offs + tp.nseg() : 0;
   // two look-back status buffers, each room for one 64-bit word per entry
-  return (size_t)(hist + offs + bins + 4 * status + (npass + 1) * tp.nseg());
+  return (size_t)(hist + offs + bins + 4 * status + (npass + 1) * tp.nseg() + bucket);
 }
 
 template <typename U>
@@ -835,9 +1036,18 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   const int nt0 = (int)((tp.T + tt - 1) / tt);
   const int nsct = (int)scatter0_tiles(tp);
   const int m = (kSortThreads * kScatter0Items) / tt;  // pack tiles per scatter tile
-  const int64_t hist_words = tp.nseg() * nt0 * npass * kRadix;
-  const int64_t offs_words = tp.nseg() * nsct * kRadix;
-  const int64_t bin_words = tp.nseg() * npass * kRadix;
+  // With link_seg and 32-bit keys the last pass links instead of sorting and
+  // needs no digit offsets.  With two passes and short segments each segment
+  // picks its link on the device (bucket_mode): by buckets of the high digit
+  // after one scatter by that digit, unless a bucket is too large for one
+  // block, then by look-back after a scatter by the low digit.
+  const bool fuse_link = link_seg && sizeof(U) == 4 && npass >= 2;
+  const bool bucket = bucket_mode(tp, sizeof(U), nt0) && fuse_link;
+  const int nh = bucket ? npass : (fuse_link ? npass - 1 : npass);
+  const int64_t hist_words = tp.nseg() * nt0 * nh * kRadix;
+  const int64_t offs_pass = tp.nseg() * nsct * kRadix;
+  const int64_t offs_words = offs_pass * (bucket ? 2 : 1);
+  const int64_t bin_words = tp.nseg() * nh * kRadix;
   const int nts = (int)sweep_tiles(tp);
   const int64_t entries = tp.nseg() * nts * kRadix;  // look-back entries of one pass
   const int64_t status_words = 2 * entries;           // a buffer holds 64-bit entries
@@ -847,6 +1057,7 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   uint32_t* status[2] = {binbase + bin_words, binbase + bin_words + status_words};
   uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then the error word
   uint32_t* err = tickets + (int64_t)npass * tp.nseg();
+  uint32_t* modes = bucket ? err + tp.nseg() : nullptr;  // after the ticket rows and error row
   const int64_t nlogical = tp.B * nt0 * ncg;
   const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
   // Divisors of the pack index math (the last head group / time tile of a row
@@ -854,7 +1065,7 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   const FastDiv by_cc = make_fastdiv((uint32_t)pl.CC), by_tt = make_fastdiv((uint32_t)tt);
   hipError_t e = with_addr(addr, tp, [&](auto src) {
     pack_hist_kernel<U, decltype(src)><<<pgrid, kPackThreads, 0, s>>>(
-        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, npass,
+        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0, nh,
         nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
     return hipGetLastError();
   });
@@ -864,39 +1075,49 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   // 1024-thread block per segment.
   if (nt0 <= kShortMaxTiles) {
     const int lm = __builtin_ctz((unsigned)m);
-    seg_offsets_kernel<<<(unsigned)(tp.nseg() * npass), kSortThreads, 0, s>>>(
-        hist, nt0, lm, npass, offs, nsct, binbase, tickets, tp.nseg());
+    seg_offsets_kernel<<<(unsigned)(tp.nseg() * nh), kSortThreads, 0, s>>>(
+        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg(), bucket ? 2 : 1, modes,
+        (uint32_t)(kLinkWaves * kLinkRun));
   } else {
-    scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, npass, offs, nsct, binbase,
-                                                           tickets);
+    scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, nh, npass, offs, nsct,
+                                                           binbase, tickets);
   }
   const int64_t nblk0 = tp.nseg() * nsct;
   const unsigned g0 = xcd_grid(nblk0, 1, (int64_t)1 << 31);
   uint32_t* next0 = npass > 1 ? status[0] : nullptr;
   scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
-      ka, kb, offs, binbase, npass, tp.T, nsct, nblk0, tp.tbits, next0, status_words);
+      ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words, modes,
+      offs_pass);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (bucket) {
+    const int nbuck = 1 << (tp.abits - 8);
+    const int ngrp = (nbuck + kLinkWaves - 1) / kLinkWaves;
+    const int64_t nlog = tp.nseg() * ngrp;
+    bucket_link_kernel<<<xcd_grid(nlog, 1, (int64_t)1 << 31), kLinkThreads, 0, s>>>(
+        (const uint32_t*)kb, binbase, tp.T, tp.C, tp.tbits, nbuck, ngrp, nlog, link_seg, modes);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   U* cur = kb;
   U* alt = ka;
   const int64_t nblks = tp.nseg() * nts;
   const unsigned gs = xcd_grid(nblks, 1, (int64_t)1 << 31);
-  // With link_seg, the last pass (32-bit keys, at least two passes) also
-  // links every record to its same-address predecessor and writes no keys.
-  const bool fuse_link = link_seg && sizeof(U) == 4 && npass >= 2;
+  // With link_seg, the last pass (32-bit keys, at least three passes here)
+  // also links every record to its same-address predecessor and writes no keys.
   for (int p = 1; p < npass; ++p) {
     uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
     if (fuse_link && p == npass - 1) {
       sweep_link_kernel<kSweepItems><<<gs, kSortThreads, 0, s>>>(
           (const uint32_t*)cur, (uint64_t*)status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T,
-          tp.C, nts, nblks, tp.tbits + 8 * p, tp.tbits, err, link_seg);
+          tp.C, nts, nblks, tp.tbits + 8 * p, tp.tbits, err, link_seg, modes);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
       *sorted = nullptr;
       return hipSuccess;
     }
     sweep_kernel<U, kSweepItems><<<gs, kSortThreads, 0, s>>>(
-        cur, alt, binbase + p * kRadix, npass,
+        cur, alt, binbase + p * kRadix, nh,
         status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T, nts, nblks, tp.tbits + 8 * p, next,
         status_words, err);
     e = hipGetLastError();

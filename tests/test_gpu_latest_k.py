@@ -340,3 +340,48 @@ def test_fused_and_generic_sorts_agree(device, shape):
     if B * T * C <= 1 << 20:
         okeys, oorder = oracle.sort_order(w, address_space=A, write_mask=m)
         assert np.array_equal(outs[0][1].cpu().numpy(), oorder)
+
+
+# ------------------------------------------ buckets that span many pieces --
+# With two 8-bit address digits, k = 1 and reads = writes, the link groups each
+# stream's records by the high address digit (a bucket): one wave walks a
+# bucket of up to 1024 records, a block of 16 waves a bucket of up to 16384,
+# and a stream with a larger bucket is linked by the look-back sweep instead.
+# These cases put many records into few buckets, and mix both kinds of stream.
+
+def _hot_case(name, T, A, C=2, B=2):
+    g = torch.Generator().manual_seed(T + A + len(name))
+    if name == "one_address":
+        w = torch.full((B, T, C), 7, dtype=torch.long)
+    elif name == "two_digits_one_bucket":  # same high digit, low digits 3 and 200
+        w = torch.where(torch.rand(B, T, C, generator=g) < 0.5, 3, 200)
+    elif name == "rare_digit":  # a low digit seen once early and once late in a hot bucket
+        w = torch.full((B, T, C), 5, dtype=torch.long)
+        w[:, 3, :] = 9
+        w[:, T - 2, :] = 9
+    elif name == "skewed":  # 90% of records at one address, the rest spread
+        w = torch.randint(0, A, (B, T, C), generator=g)
+        w = torch.where(torch.rand(B, T, C, generator=g) < 0.9, torch.zeros_like(w), w)
+    elif name == "few_buckets":  # A = 512: two buckets of ~T/2 records
+        w = torch.randint(0, A, (B, T, C), generator=g)
+    elif name == "mixed_modes":  # head 0 one hot address, head 1 uniform: both links in one call
+        w = torch.randint(0, A, (B, T, C), generator=g)
+        w[:, :, 0] = 11
+    else:
+        raise ValueError(name)
+    return w
+
+
+HOT = [("one_address", 1024, 4096), ("one_address", 1025, 4096), ("one_address", 2048, 4096),
+       ("one_address", 70000 // 2, 65536), ("two_digits_one_bucket", 5000, 256 * 256),
+       ("rare_digit", 20000, 4096), ("skewed", 30000, 65536), ("few_buckets", 40000, 512),
+       ("few_buckets", 3000, 300)]
+
+
+@pytest.mark.parametrize("case", HOT, ids=[f"{n}-{T}-{A}" for n, T, A in HOT])
+def test_multi_piece_buckets(device, case):
+    name, T, A = case
+    print(f"[hot buckets] {name} T={T} A={A}", flush=True)
+    w = _hot_case(name, T, A)
+    p = torch.randn(*w.shape, 8).to(torch.bfloat16)
+    check_against_oracle(w.to(device), p.to(device), A=A, k=1)
