@@ -15,6 +15,8 @@
 // the input, and LSD passes are stable, so the result is ordered by (a, t).
 
 #include "em_addr.h"
+
+#include <type_traits>
 #include "em_common.h"
 
 namespace rem {
@@ -276,13 +278,20 @@ __device__ __forceinline__ void zero_slice(uint32_t* __restrict__ p, int64_t wor
 // passes whose scatter needs offsets).  Sibling head
 // groups of one time tile are consecutive logical blocks, which xcd_block
 // places on one XCD, so the 128-byte address rows they share stay in one L2.
-template <typename U, typename AS>
+// VEC > 1: the slab's rows are whole 16-byte units (VEC addresses each, the
+// tensor 16-byte aligned), loaded and stored 16 bytes at a time.  The LDS
+// rows are TT + 8 keys apart, which spreads a wave's stores of 4 to 16 heads
+// over the banks.
+constexpr int kPackPad = 8;
+constexpr int kPackBatchV = 8;  // 16-byte address loads in flight per pack thread
+
+template <typename U, typename AT, int VEC>
 __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
-    const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
+    const DenseAddr<AT> addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int h0, int nh, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
     uint32_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
-  __shared__ U tile[kPackLdsBytes / sizeof(U)];
+  __shared__ __align__(16) U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
   zero_slice(zero, zero_words);  // every block, padding included
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
@@ -296,12 +305,47 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
   const int64_t t0 = (int64_t)tb * TT;
   const int tt = (int)((T - t0) < TT ? (T - t0) : TT);
   const int n = tt * cc;
-  const int pitch = TT + 1;
+  const int pitch = TT + kPackPad;
   const int per = nh * kRadix;
   const int hshift = tbits + 8 * h0;
   const int hw = cc * per;
   for (int i = threadIdx.x; i < hw; i += kPackThreads) h[i] = 0;
   __syncthreads();
+  auto put = [&](int64_t av, int tl, int cl) {
+    int64_t a = reduce_addr(av, A, mode, trunc32 != 0);
+    if (wmask && !wmask[b * T + t0 + tl]) a = A;
+    const U u = ((U)a << tbits) | (U)(t0 + tl);
+    tile[cl * pitch + tl] = u;
+    for (int p = 0; p < nh; ++p)
+      atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (hshift + 8 * p)) & (kRadix - 1))], 1u);
+  };
+  if constexpr (VEC > 1) {
+    // by_cc divides by the 16-byte units of a full head group's row here
+    const int nv = cc / VEC;
+    const int nu = tt * nv;
+    const AT* base = addr.p + ((b * T + t0) * C + c0);
+    for (int i0 = 0; i0 < nu; i0 += kPackThreads * kPackBatchV) {
+      u32x4 v[kPackBatchV];
+#pragma unroll
+      for (int j = 0; j < kPackBatchV; ++j) {
+        const int i = i0 + j * kPackThreads + threadIdx.x;
+        const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)nv);
+        if (i < nu) v[j] = *(const u32x4*)(base + (int64_t)tl * C + (i - tl * nv) * VEC);
+      }
+#pragma unroll
+      for (int j = 0; j < kPackBatchV; ++j) {
+        const int i = i0 + j * kPackThreads + threadIdx.x;
+        if (i < nu) {
+          const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)nv);
+          const int cv = (i - tl * nv) * VEC;
+          AT el[VEC];
+          __builtin_memcpy(el, &v[j], sizeof(el));
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) put((int64_t)el[e], tl, cv + e);
+        }
+      }
+    }
+  } else {
   for (int i0 = 0; i0 < n; i0 += kPackThreads * kPackBatch) {
     int64_t av[kPackBatch];
 #pragma unroll
@@ -315,21 +359,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
       const int i = i0 + j * kPackThreads + threadIdx.x;
       if (i < n) {
         const int tl = (int)fdiv_or((uint32_t)i, by_cc, (uint32_t)cc);
-        const int cl = i - tl * cc;
-        int64_t a = reduce_addr(av[j], A, mode, trunc32 != 0);
-        if (wmask && !wmask[b * T + t0 + tl]) a = A;
-        const U u = ((U)a << tbits) | (U)(t0 + tl);
-        tile[cl * pitch + tl] = u;
-        for (int p = 0; p < nh; ++p)
-          atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (hshift + 8 * p)) & (kRadix - 1))], 1u);
+        put(av[j], tl, i - tl * cc);
       }
     }
   }
+  }
   __syncthreads();
-  for (int i = threadIdx.x; i < n; i += kPackThreads) {
-    const int cl = (int)fdiv_or((uint32_t)i, by_tt, (uint32_t)tt);
-    const int tl = i - cl * tt;
-    keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
+  if (VEC > 1 && sizeof(U) == 4 && (tt & 3) == 0 && (T & 3) == 0) {
+    // 4 keys per 16-byte LDS read and global store (rows start 16-byte aligned)
+    const int q = tt >> 2;
+    for (int i = threadIdx.x; i < cc * q; i += kPackThreads) {
+      const int cl = i / q;
+      const int tq = (i - cl * q) << 2;
+      *(u32x4*)&keys[(b * C + c0 + cl) * T + t0 + tq] = *(const u32x4*)&tile[cl * pitch + tq];
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += kPackThreads) {
+      const int cl = (int)fdiv_or((uint32_t)i, by_tt, (uint32_t)tt);
+      const int tl = i - cl * tt;
+      keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
+    }
   }
   // hist layout [seg][tile][pass][256]: one contiguous nh KB run per head.
   for (int i = threadIdx.x; i < hw; i += kPackThreads) {
@@ -806,15 +855,17 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
 // A wave's LDS operations execute in issue order, so every read sees exactly
 // the writes of earlier steps and of this step's earlier instructions.
 //
-// The block of logical id (seg, g) owns buckets 16g..16g+15 of segment seg.
+// The block of logical id (seg, g) owns buckets 8g..8g+7 of segment seg.
 // A bucket of at most kLinkRun keys is one run of one wave (wave w takes
-// bucket 16g + w; uniform addresses put ~T/256 keys in a bucket).  A larger
-// bucket is walked by all 16 waves of the block together, in rounds of 16
+// bucket 8g + w; uniform addresses put ~T/256 keys in a bucket).  A larger
+// bucket is walked by all 8 waves of the block together, in rounds of 8
 // runs: after a round a block barrier, then per digit the last time before
 // each wave's run (from earlier waves' tables and a running carry over the
 // rounds), then each wave resolves the keys of its run that had no
-// predecessor inside the run.  No look-back, no wait on another block.
-constexpr int kLinkWaves = 16;
+// predecessor inside the run.  No look-back, no wait on another block.  A
+// segment with a bucket of more than one round's keys links by look-back
+// instead (the offsets kernel decides).
+constexpr int kLinkWaves = 8;
 constexpr int kLinkThreads = kLinkWaves * kWave;
 constexpr int kLinkSteps = 16;
 constexpr int kLinkRun = kLinkSteps * kWave;  // keys of one wave's run
@@ -981,7 +1032,11 @@ PackPlan fused_plan(const Tape& tp, size_t key_bytes) {
   int tt = kSortThreads * kScatter0Items;  // a pack tile divides the 2048-key scatter tile
   while (tt > 64 && tt / 2 >= tp.T) tt >>= 1;  // short tapes: smaller pack tiles
   const int64_t cap = (int64_t)(kPackLdsBytes / key_bytes);
-  int64_t cc = cap / (tt + 1);
+  // Wider head groups (whole address rows read once) while the segment keeps
+  // at most kShortMaxTiles pack tiles.
+  while (tt > 256 && cap / (tt + kPackPad) < tp.C && (tp.T + tt / 2 - 1) / (tt / 2) <= kShortMaxTiles)
+    tt >>= 1;
+  int64_t cc = cap / (tt + kPackPad);
   if (cc > tp.C) cc = tp.C;
   if (cc * npass * kRadix > kHistWords) cc = kHistWords / (npass * kRadix);
   if (cc < 1) return pl;
@@ -1062,11 +1117,23 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
   // Divisors of the pack index math (the last head group / time tile of a row
   // may be smaller and then divides the slow way).
-  const FastDiv by_cc = make_fastdiv((uint32_t)pl.CC), by_tt = make_fastdiv((uint32_t)tt);
+  const FastDiv by_tt = make_fastdiv((uint32_t)tt);
   hipError_t e = with_addr(addr, tp, [&](auto src) {
-    pack_hist_kernel<U, decltype(src)><<<pgrid, kPackThreads, 0, s>>>(
-        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0, nh,
-        nt0, nlogical, by_cc, by_tt, ka, hist, zero, zero_words);
+    using AT = std::remove_cv_t<std::remove_pointer_t<decltype(src.p)>>;
+    constexpr int VEC = 16 / (int)sizeof(AT);
+    // 16-byte loads when every head group's row is whole 16-byte units
+    const bool vec = (uintptr_t)src.p % 16 == 0 && (tp.C * (int64_t)sizeof(AT)) % 16 == 0 &&
+                     (pl.CC * (int64_t)sizeof(AT)) % 16 == 0;
+    if (vec) {
+      pack_hist_kernel<U, AT, VEC><<<pgrid, kPackThreads, 0, s>>>(
+          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
+          nh, nt0, nlogical, make_fastdiv((uint32_t)(pl.CC / VEC)), by_tt, ka, hist, zero,
+          zero_words);
+    } else {
+      pack_hist_kernel<U, AT, 1><<<pgrid, kPackThreads, 0, s>>>(
+          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
+          nh, nt0, nlogical, make_fastdiv((uint32_t)pl.CC), by_tt, ka, hist, zero, zero_words);
+    }
     return hipGetLastError();
   });
   if (e != hipSuccess) return e;

@@ -345,7 +345,7 @@ def test_fused_and_generic_sorts_agree(device, shape):
 # ------------------------------------------ buckets that span many pieces --
 # With two 8-bit address digits, k = 1 and reads = writes, the link groups each
 # stream's records by the high address digit (a bucket): one wave walks a
-# bucket of up to 1024 records, a block of 16 waves a bucket of up to 16384,
+# bucket of up to 1024 records, a block of 8 waves a bucket of up to 8192,
 # and a stream with a larger bucket is linked by the look-back sweep instead.
 # These cases put many records into few buckets, and mix both kinds of stream.
 
