@@ -347,7 +347,8 @@ def test_fused_and_generic_sorts_agree(device, shape):
 # stream's records by the high address digit (a bucket): one wave walks a
 # bucket of up to 1024 records, a block of 8 waves a bucket of up to 8192,
 # and a stream with a larger bucket is linked by the look-back sweep instead.
-# These cases put many records into few buckets, and mix both kinds of stream.
+# These cases put many records into few buckets, at those boundaries, and mix
+# both kinds of stream in one call.
 
 def _hot_case(name, T, A, C=2, B=2):
     g = torch.Generator().manual_seed(T + A + len(name))
@@ -373,6 +374,7 @@ def _hot_case(name, T, A, C=2, B=2):
 
 
 HOT = [("one_address", 1024, 4096), ("one_address", 1025, 4096), ("one_address", 2048, 4096),
+       ("one_address", 8192, 4096), ("one_address", 8193, 4096), ("one_address", 16385, 4096),
        ("one_address", 70000 // 2, 65536), ("two_digits_one_bucket", 5000, 256 * 256),
        ("rare_digit", 20000, 4096), ("skewed", 30000, 65536), ("few_buckets", 40000, 512),
        ("few_buckets", 3000, 300)]
