@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const DenseAddr<AT> addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int h0, int nh, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
-    uint32_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
+    uint16_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
   __shared__ __align__(16) U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
   zero_slice(zero, zero_words);  // every block, padding included
@@ -380,18 +380,18 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
       keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
     }
   }
-  // hist layout [seg][tile][pass][256]: one contiguous nh KB run per head.
+  // hist layout [seg][tile][pass][256] of 16-bit counts: one contiguous run per head.
   for (int i = threadIdx.x; i < hw; i += kPackThreads) {
     const int cl = i / per;
     const int r = i - cl * per;
-    hist[(((b * C + c0 + cl) * ntiles + tb) * (int64_t)per) + r] = h[i];
+    hist[(((b * C + c0 + cl) * ntiles + tb) * (int64_t)per) + r] = (uint16_t)h[i];
   }
 }
 
 // Per segment: digit bases of every pass, and the pass-0 offsets of each
 // scatter tile (m consecutive pack tiles): offs[seg][tile][d] = count of digit d
 // in the segment's earlier scatter tiles.  Also resets the look-back tickets.
-__global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restrict__ hist,
+__global__ __launch_bounds__(1024) void scan_hist_kernel(const uint16_t* __restrict__ hist,
                                                         int ntiles, int m, int nh, int npass,
                                                         uint32_t* __restrict__ offs, int nsct,
                                                         uint32_t* __restrict__ binbase,
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint32_t* __restr
   const int g = threadIdx.x / kRadix;
   const int64_t seg = blockIdx.x;
   const int per = nh * kRadix;
-  const uint32_t* hs = hist + seg * (int64_t)ntiles * per;
+  const uint16_t* hs = hist + seg * (int64_t)ntiles * per;
   // group g owns whole scatter tiles [slo, shi), i.e. pack tiles [slo*m, shi*m)
   const int slen = (nsct + G - 1) / G;
   const int slo = g * slen < nsct ? g * slen : nsct;
@@ -553,7 +553,7 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
 constexpr int kShortMaxTiles = 64;
 
 __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
-    const uint32_t* __restrict__ hist, int nt0, int lm, int nh, int npass,
+    const uint16_t* __restrict__ hist, int nt0, int lm, int nh, int npass,
     uint32_t* __restrict__ offs, int nsct, uint32_t* __restrict__ binbase,
     uint32_t* __restrict__ tickets, int64_t nseg, int noffs, uint32_t* __restrict__ modes,
     uint32_t bucket_max) {
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
   const int64_t seg = blockIdx.x / nh;
   const int p = (int)(blockIdx.x - seg * nh);
   const int per = nh * kRadix;
-  const uint32_t* hs = hist + seg * (int64_t)nt0 * per + p * kRadix + d;
+  const uint16_t* hs = hist + seg * (int64_t)nt0 * per + p * kRadix + d;
   uint32_t v[kShortMaxTiles];
 #pragma unroll
   for (int j = 0; j < kShortMaxTiles; ++j) v[j] = j < nt0 ? hs[(int64_t)j * per] : 0u;
@@ -1106,8 +1106,9 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   const int nts = (int)sweep_tiles(tp);
   const int64_t entries = tp.nseg() * nts * kRadix;  // look-back entries of one pass
   const int64_t status_words = 2 * entries;           // a buffer holds 64-bit entries
-  uint32_t* hist = words;
-  uint32_t* offs = hist + hist_words;
+  // pack-tile histograms hold counts <= TT < 2^16: 16-bit words, two a word
+  uint16_t* hist = (uint16_t*)words;
+  uint32_t* offs = words + (hist_words + 1) / 2;
   uint32_t* binbase = offs + offs_words;
   uint32_t* status[2] = {binbase + bin_words, binbase + bin_words + status_words};
   uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then the error word
