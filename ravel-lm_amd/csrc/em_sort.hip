@@ -467,15 +467,20 @@ __device__ __forceinline__ void load_tile(const U* __restrict__ src, int n, U* k
   }
 }
 
-// Keys must come from load_tile (wave-striped ownership).
-template <typename U, int ITEMS>
+// Keys must come from load_tile (wave-striped ownership).  NT threads (a
+// multiple of 256); the per-digit steps run on threads 0..255.
+template <typename U, int ITEMS, int NT = kSortThreads>
 __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRadix],
                                           uint32_t* dstart, uint32_t* scan_tmp, const U* key,
                                           uint32_t* rank, uint32_t* own) {
-  constexpr int NW = kSortThreads / kWave;
+  constexpr int NW = NT / kWave;
+  static_assert(NT % kRadix == 0, "whole digit rows per thread group");
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) wcnt[i][tid] = 0;
+  for (int i = 0; i < NW * kRadix / NT; ++i) {
+    const int x = i * NT + tid;
+    wcnt[x / kRadix][x % kRadix] = 0;
+  }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
@@ -494,14 +499,17 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
   }
   __syncthreads();
   uint32_t tot = 0;
+  if (tid < kRadix) {
 #pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const uint32_t c = wcnt[i][tid];
-    wcnt[i][tid] = tot;
-    tot += c;
+    for (int i = 0; i < NW; ++i) {
+      const uint32_t c = wcnt[i][tid];
+      wcnt[i][tid] = tot;
+      tot += c;
+    }
   }
   *own = tot;
-  dstart[tid] = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
+  const uint32_t ex = block_excl_scan<NT>(tot, scan_tmp, nullptr);
+  if (tid < kRadix) dstart[tid] = ex;
 }
 
 // Stage the ranked tile in LDS in local sorted order, then write each digit's
@@ -724,30 +732,22 @@ constexpr uint64_t kLFlagP = 2ull << 62;
 constexpr uint64_t kLHasKey = 1ull << 61;
 constexpr uint64_t kLCountMask = (1ull << 29) - 1;
 
-template <int ITEMS>
-__global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
+// One tile of the link sweep on NT threads (the standalone kernel runs 256,
+// the bucket link's look-back segments 512); the LDS arrays come from the
+// caller.
+template <int ITEMS, int NT>
+__device__ __forceinline__ void sweep_link_tile(
     const uint32_t* __restrict__ in, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ ticket, int64_t T, int64_t C, int ntiles, int64_t nblk, int shift,
+    uint32_t* __restrict__ ticket, int64_t T, int64_t C, int ntiles, int64_t seg, int shift,
     int tbits, uint32_t* __restrict__ err, int32_t* __restrict__ src_seg,
-    const uint32_t* __restrict__ modes) {
+    uint32_t (*wcnt)[kRadix], uint32_t* dstart, uint32_t* scan_tmp, uint32_t* s_ticket,
+    uint32_t* carry_key, uint8_t* carry_has, uint32_t* stage) {
   using U = uint32_t;
-  constexpr int NW = kSortThreads / kWave;
-  constexpr int TILE = kSortThreads * ITEMS;
-  __shared__ uint32_t wcnt[NW][kRadix];
-  __shared__ uint32_t dstart[kRadix];
-  __shared__ uint32_t scan_tmp[NW + 1];
-  __shared__ uint32_t s_ticket;
-  __shared__ uint32_t carry_key[kRadix];
-  __shared__ uint8_t carry_has[kRadix];
-  __shared__ U stage[TILE];
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
-  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
-  if (lb >= nblk) return;  // uniform per block
-  const int64_t seg = lb / ntiles;
-  if (modes && modes[seg]) return;  // uniform per block: this segment links by buckets
-  if (tid == 0) s_ticket = atomicAdd(&ticket[seg], 1u);
+  constexpr int TILE = NT * ITEMS;
+  if (tid == 0) *s_ticket = atomicAdd(&ticket[seg], 1u);
   __syncthreads();
-  const int tile = (int)s_ticket;
+  const int tile = (int)*s_ticket;
   if (tile >= ntiles) return;  // uniform per block; tickets run 0..ntiles-1
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
@@ -755,7 +755,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  rank_tile<U, ITEMS, NT>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
   __syncthreads();  // dstart of every digit
   // The tile in local sorted order (digit runs in order).
 #pragma unroll
@@ -767,54 +767,56 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
     }
   }
   __syncthreads();
-  const uint32_t own_last = own ? stage[dstart[tid] + own - 1] : 0u;
-  uint64_t* st = status + (seg * ntiles) * (int64_t)kRadix;
-  const uint64_t agg = (own ? (kLHasKey | own_last) : 0ull) | ((uint64_t)own << 32);
-  __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], (tile == 0 ? kLFlagP : kLFlagA) | agg,
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint32_t excl = 0, lastk = 0;
-  bool found = false, ok = true, done = tile == 0;
-  for (int hi = tile - 1; !done && hi >= 0; hi -= kLookBatch) {
-    uint64_t v[kLookBatch];
+  if (tid < kRadix) {
+    const uint32_t own_last = own ? stage[dstart[tid] + own - 1] : 0u;
+    uint64_t* st = status + (seg * ntiles) * (int64_t)kRadix;
+    const uint64_t agg = (own ? (kLHasKey | own_last) : 0ull) | ((uint64_t)own << 32);
+    __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], (tile == 0 ? kLFlagP : kLFlagA) | agg,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t excl = 0, lastk = 0;
+    bool found = false, ok = true, done = tile == 0;
+    for (int hi = tile - 1; !done && hi >= 0; hi -= kLookBatch) {
+      uint64_t v[kLookBatch];
 #pragma unroll
-    for (int j = 0; j < kLookBatch; ++j)
-      v[j] = (hi - j >= 0) ? __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid],
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : kLFlagP;
+      for (int j = 0; j < kLookBatch; ++j)
+        v[j] = (hi - j >= 0) ? __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid],
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : kLFlagP;
 #pragma unroll
-    for (int j = 0; j < kLookBatch; ++j) {
-      if (done || hi - j < 0) continue;
-      uint64_t x = v[j];
-      int spins = 0;
-      while ((x >> 62) == 0 && spins < kSpinLimit) {
-        __builtin_amdgcn_s_sleep(1);
-        x = __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid], __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-        ++spins;
+      for (int j = 0; j < kLookBatch; ++j) {
+        if (done || hi - j < 0) continue;
+        uint64_t x = v[j];
+        int spins = 0;
+        while ((x >> 62) == 0 && spins < kSpinLimit) {
+          __builtin_amdgcn_s_sleep(1);
+          x = __hip_atomic_load(&st[(int64_t)(hi - j) * kRadix + tid], __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+          ++spins;
+        }
+        if ((x >> 62) == 0) {
+          ok = false;
+          done = true;
+          continue;
+        }
+        excl += (uint32_t)((x >> 32) & kLCountMask);
+        if (!found && (x & kLHasKey)) {
+          found = true;
+          lastk = (uint32_t)x;
+        }
+        if ((x >> 62) == 2) done = true;
       }
-      if ((x >> 62) == 0) {
-        ok = false;
-        done = true;
-        continue;
-      }
-      excl += (uint32_t)((x >> 32) & kLCountMask);
-      if (!found && (x & kLHasKey)) {
-        found = true;
-        lastk = (uint32_t)x;
-      }
-      if ((x >> 62) == 2) done = true;
     }
+    if (!ok) atomicOr(err, 1u);
+    if (tile > 0) {
+      const bool has = own || found;
+      const uint64_t inc = (has ? kLHasKey : 0ull) | (uint64_t)(own ? own_last : lastk) |
+                           ((uint64_t)((excl + own) & (uint32_t)kLCountMask) << 32);
+      __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kLFlagP | inc, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    carry_key[tid] = lastk;
+    carry_has[tid] = found ? 1 : 0;
   }
-  if (!ok) atomicOr(err, 1u);
-  if (tile > 0) {
-    const bool has = own || found;
-    const uint64_t inc = (has ? kLHasKey : 0ull) | (uint64_t)(own ? own_last : lastk) |
-                         ((uint64_t)((excl + own) & (uint32_t)kLCountMask) << 32);
-    __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kLFlagP | inc, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-  carry_key[tid] = lastk;
-  carry_has[tid] = found ? 1 : 0;
   __syncthreads();
   const U tmask = (U)((1u << tbits) - 1u);
   const int64_t b = seg / C, c = seg - (seg / C) * C;
@@ -822,7 +824,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
   int32_t* dst = src_seg + seg * T;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    const int idx = i * kSortThreads + tid;
+    const int idx = i * NT + tid;
     if (idx < n) {
       const U u = stage[idx];
       const uint32_t d = (u >> shift) & (kRadix - 1);
@@ -833,6 +835,26 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
       dst[u & tmask] = v;
     }
   }
+}
+
+template <int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
+    const uint32_t* __restrict__ in, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ ticket, int64_t T, int64_t C, int ntiles, int64_t nblk, int shift,
+    int tbits, uint32_t* __restrict__ err, int32_t* __restrict__ src_seg) {
+  constexpr int NW = kSortThreads / kWave;
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ uint32_t s_ticket;
+  __shared__ uint32_t carry_key[kRadix];
+  __shared__ uint8_t carry_has[kRadix];
+  __shared__ uint32_t stage[kSortThreads * ITEMS];
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  sweep_link_tile<ITEMS, kSortThreads>(in, status, ticket, T, C, ntiles, lb / ntiles, shift, tbits,
+                                       err, src_seg, wcnt, dstart, scan_tmp, &s_ticket, carry_key,
+                                       carry_has, stage);
 }
 
 // Read == write, k == 1, 32-bit keys, two digit passes: the link without a
@@ -928,10 +950,14 @@ __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, in
   return first;
 }
 
+// Segments that chose the look-back link (modes[seg] == 0) run it here too:
+// the block of logical id (seg, g < ntiles) is one sweep tile of kSweepTile
+// keys on the block's 512 threads, in the same LDS.
 __global__ __launch_bounds__(kLinkThreads) void bucket_link_kernel(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ binbase, int64_t T,
     int64_t C, int tbits, int nbuck, int ngrp, int64_t nlogical, int32_t* __restrict__ src_seg,
-    const uint32_t* __restrict__ modes) {
+    const uint32_t* __restrict__ modes, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ ticket, int ntiles, uint32_t* __restrict__ err) {
   __shared__ __align__(16) uint64_t mtab[kLinkWaves][kRadix];  // all zero between steps
   __shared__ __align__(16) uint32_t ltab[kLinkWaves][kRadix];  // kLHas32 | time, 0 = none
   __shared__ __align__(16) uint32_t ctab[kLinkWaves][kRadix];  // carry into a wave's run
@@ -941,8 +967,18 @@ __global__ __launch_bounds__(kLinkThreads) void bucket_link_kernel(
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
   if (logical >= nlogical) return;  // uniform per block
   const int64_t seg = logical / ngrp;
-  if (!modes[seg]) return;  // uniform per block: this segment links by look-back
-  const int b0 = (int)(logical - seg * ngrp) * kLinkWaves;
+  const int g = (int)(logical - seg * ngrp);
+  if (!modes[seg]) {  // uniform per block: this segment links by look-back
+    static_assert(kLinkThreads * (kSweepTile / kLinkThreads) == kSweepTile, "sweep tile");
+    static_assert(sizeof(mtab) >= kSweepTile * sizeof(uint32_t), "stage in mtab");
+    static_assert(sizeof(ctab) >= 4 * kRadix * sizeof(uint32_t), "small arrays in ctab");
+    if (g >= ntiles) return;
+    sweep_link_tile<kSweepTile / kLinkThreads, kLinkThreads>(
+        keys, status, ticket, T, C, ntiles, seg, tbits + 8, tbits, err, src_seg, ltab, ctab[0],
+        ctab[3], &ctab[4][0], ctab[1], (uint8_t*)ctab[2], (uint32_t*)&mtab[0][0]);
+    return;
+  }
+  const int b0 = g * kLinkWaves;
   const uint32_t* bb = binbase + (seg * 2 + 1) * kRadix;  // the high digit's bucket starts
   if (tid <= kLinkWaves) {
     const int x = b0 + tid;
@@ -1159,26 +1195,32 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (bucket) {
+    // one launch for both links: buckets for most segments, look-back tiles for the rest
     const int nbuck = 1 << (tp.abits - 8);
-    const int ngrp = (nbuck + kLinkWaves - 1) / kLinkWaves;
+    int ngrp = (nbuck + kLinkWaves - 1) / kLinkWaves;
+    if (ngrp < nts) ngrp = nts;
     const int64_t nlog = tp.nseg() * ngrp;
     bucket_link_kernel<<<xcd_grid(nlog, 1, (int64_t)1 << 31), kLinkThreads, 0, s>>>(
-        (const uint32_t*)kb, binbase, tp.T, tp.C, tp.tbits, nbuck, ngrp, nlog, link_seg, modes);
+        (const uint32_t*)kb, binbase, tp.T, tp.C, tp.tbits, nbuck, ngrp, nlog, link_seg, modes,
+        (uint64_t*)status[0], tickets + tp.nseg(), nts, err);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    *sorted = nullptr;
+    return hipSuccess;
   }
   U* cur = kb;
   U* alt = ka;
   const int64_t nblks = tp.nseg() * nts;
   const unsigned gs = xcd_grid(nblks, 1, (int64_t)1 << 31);
-  // With link_seg, the last pass (32-bit keys, at least three passes here)
-  // also links every record to its same-address predecessor and writes no keys.
+  // With link_seg, the last pass (32-bit keys, three or more passes or long
+  // segments here) also links every record to its same-address predecessor
+  // and writes no keys.
   for (int p = 1; p < npass; ++p) {
     uint32_t* next = (p + 1 < npass) ? status[p % 2] : nullptr;
     if (fuse_link && p == npass - 1) {
       sweep_link_kernel<kSweepItems><<<gs, kSortThreads, 0, s>>>(
           (const uint32_t*)cur, (uint64_t*)status[(p - 1) % 2], tickets + p * tp.nseg(), tp.T,
-          tp.C, nts, nblks, tp.tbits + 8 * p, tp.tbits, err, link_seg, modes);
+          tp.C, nts, nblks, tp.tbits + 8 * p, tp.tbits, err, link_seg);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
       *sorted = nullptr;
