@@ -245,6 +245,19 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
+  if (link && link_short_applies(tp, k)) {  // short tapes: sort and link per segment in LDS
+    stage_begin(kStageSort, s);
+    AddrIn wd;
+    hipError_t e = compact_addresses(wa, tp, sw.kb, &wd, s);
+    if (e == hipSuccess) e = link_short(wd, tp, (int)k, src, s);
+    stage_end(kStageSort, s);
+    if (e != hipSuccess) return hip_fail(e, "sort");
+    stage_begin(kStageGather, s);
+    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+    stage_end(kStageGather, s);
+    if (e != hipSuccess) return hip_fail(e, "gather");
+    return RAVEL_EM_OK;
+  }
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
   hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
@@ -277,6 +290,13 @@ int resolve_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   SortWs<U> sw = take_sort<U>(bp, tp);
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
+  if (link && link_short_applies(tp, k)) {  // short tapes: sort and link per segment in LDS
+    AddrIn wd;
+    hipError_t e = compact_addresses(wa, tp, sw.kb, &wd, s);
+    if (e == hipSuccess) e = link_short(wd, tp, (int)k, src, s);
+    if (e != hipSuccess) return hip_fail(e, "sort");
+    return RAVEL_EM_OK;
+  }
   U* sorted = nullptr;
   hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
                               link && k == 1 ? src_seg : nullptr);

@@ -217,6 +217,11 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 // search_reads writes record-major ([B,T,C,k]).
 template <typename U>
 hipError_t link_same(const U* sorted, const Tape& tp, int k, int32_t* src_seg, hipStream_t s);
+// read == write, no write mask, short tapes (link_short_applies): the whole
+// sort and the link per segment in LDS, record-major sources ([B,T,C,k]) from
+// the address tensor in one kernel.
+bool link_short_applies(const Tape& tp, int64_t k);
+hipError_t link_short(const AddrIn& addr, const Tape& tp, int k, int32_t* src, hipStream_t s);
 // read == write with every head of a batch row in LDS (link_rows_applies):
 // the sources record-major ([B,T,C,k]) in one kernel.
 bool link_rows_applies(const Tape& tp, int k, size_t key_bytes);

@@ -1240,10 +1240,25 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   return hipSuccess;
 }
 
+bool sort_short_applies(const Tape& tp);
+template <bool LINK>
+hipError_t seg_sort_short(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, int k,
+                          int32_t* src, uint32_t* keys_out, hipStream_t s);
+
 template <typename U>
 hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, U* ka,
                      U* kb, uint32_t* counts, U** sorted, hipStream_t s, uint32_t* zero,
                      int64_t zero_words, int32_t* link_seg) {
+  if (sizeof(U) == 4 && tp.fused && sort_short_applies(tp)) {
+    // short tapes: each segment sorted in LDS by one block (the caller links)
+    if (zero && zero_words > 0) {
+      const hipError_t ez = fill_bytes(zero, 0, (size_t)zero_words * 4, s);
+      if (ez != hipSuccess) return ez;
+    }
+    *sorted = ka;
+    if (tp.n() == 0) return hipSuccess;
+    return seg_sort_short<false>(addr, wmask, tp, 0, nullptr, (uint32_t*)ka, s);
+  }
   if (tp.fused) {
     const PackPlan pl = fused_plan(tp, sizeof(U));
     if (pl.TT)
@@ -1303,6 +1318,167 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
     emit_order_kernel<U, int32_t><<<grid, 256, 0, s>>>(sorted, vp, N, tp.T, tp.C, tp.A, tp.tbits,
                                                        (int32_t*)out_keys, out_order);
   return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// Short tapes (T <= kShortT, 32-bit keys): one block per segment (b, c) sorts
+// the segment's keys in LDS (stable LSD passes of the address digits over
+// keys a << tbits | t built in time order; a masked record gets address A).
+// One launch replaces the key build, the offsets and the scatter passes of
+// the global sort, which on short tapes are each a few microseconds of
+// latency for little data.  Without LINK the sorted keys go out
+// segment-major, as the global sort leaves them.  With LINK (read == write,
+// no mask) the block inverts the order (time -> sorted position) in LDS and
+// writes each record's k latest same-address sources record-major
+// ([B,T,C,k]), k consecutive words per record.  The segments of one batch row
+// are consecutive logical blocks on one XCD, so the partial lines of their
+// interleaved output rows merge in one L2.
+namespace {
+
+constexpr int kShortT = 4096;
+constexpr int kShortItems = kShortT / kSortThreads;
+
+template <typename AS, int ITEMS, bool LINK>
+__global__ __launch_bounds__(kSortThreads) void seg_sort_link_kernel(
+    const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int tbits,
+    int npass, int mode, int trunc32, int k, int64_t nseg, int32_t* __restrict__ src,
+    uint32_t* __restrict__ keys_out) {
+  constexpr int NW = kSortThreads / kWave;
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ uint32_t buf[2][kShortT];
+  __shared__ uint16_t inv[kShortT];
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  const int64_t seg = xcd_block(blockIdx.x, gridDim.x);
+  if (seg >= nseg) return;  // uniform per block
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const int n = (int)T;
+  const uint32_t tmask = (1u << tbits) - 1u;
+  // Keys in time order, wave-striped as load_tile lays them out.
+  uint32_t key[ITEMS];
+  int64_t av[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int t = w * kWave * ITEMS + i * kWave + lane;
+    av[i] = t < n ? addr(b, t, c) : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int t = w * kWave * ITEMS + i * kWave + lane;
+    int64_t a = reduce_addr(av[i], A, mode, trunc32 != 0);
+    if (wmask && t < n && !wmask[b * T + t]) a = A;
+    key[i] = t < n ? ((uint32_t)a << tbits) | (uint32_t)t : 0u;
+  }
+  uint32_t* sorted = buf[0];
+  for (int p = 0; p < npass; ++p) {
+    const int shift = tbits + 8 * p;
+    uint32_t rank[ITEMS];
+    uint32_t own;
+    rank_tile<uint32_t, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+    __syncthreads();  // dstart of every digit
+    sorted = buf[p & 1];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = w * kWave * ITEMS + i * kWave + lane;
+      if (idx < n) {
+        const uint32_t d = (key[i] >> shift) & (kRadix - 1);
+        sorted[dstart[d] + wcnt[w][d] + rank[i]] = key[i];
+      }
+    }
+    __syncthreads();
+    load_tile<uint32_t, ITEMS>(sorted, n, key);
+  }
+  if (!LINK) {  // the sorted keys (in registers, wave-striped), segment-major
+    uint32_t* o = keys_out + seg * T;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = w * kWave * ITEMS + i * kWave + lane;
+      if (idx < n) o[idx] = key[i];
+    }
+    return;
+  }
+  if (npass == 0) {  // one address: time order is the order
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = w * kWave * ITEMS + i * kWave + lane;
+      if (idx < n) sorted[idx] = key[i];
+    }
+    __syncthreads();
+  }
+  for (int p = tid; p < n; p += kSortThreads) inv[sorted[p] & tmask] = (uint16_t)p;
+  __syncthreads();
+  const int32_t base = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  for (int t = tid; t < n; t += kSortThreads) {
+    const int p = inv[t];
+    const uint32_t a = sorted[p] >> tbits;
+    int32_t* o = src + ((b * T + t) * C + c) * (int64_t)k;
+    bool alive = true;
+    auto slot = [&](int j) {
+      const int q = p - 1 - j;
+      int32_t v = -1;
+      if (alive && q >= 0) {
+        const uint32_t uq = sorted[q];
+        if ((uq >> tbits) == a)
+          v = base + (int32_t)(uq & tmask) * Ci;
+        else
+          alive = false;
+      } else {
+        alive = false;
+      }
+      return v;
+    };
+    if ((k & 3) == 0) {  // 16-byte stores (o is 16-byte aligned when k % 4 == 0)
+      for (int j = 0; j < k; j += 4) {
+        u32x4 v;
+        v.x = (uint32_t)slot(j);
+        v.y = (uint32_t)slot(j + 1);
+        v.z = (uint32_t)slot(j + 2);
+        v.w = (uint32_t)slot(j + 3);
+        *(u32x4*)(o + j) = v;
+      }
+    } else {
+      for (int j = 0; j < k; ++j) o[j] = slot(j);
+    }
+  }
+}
+
+}  // namespace
+
+template <bool LINK>
+hipError_t seg_sort_short(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, int k,
+                          int32_t* src, uint32_t* keys_out, hipStream_t s) {
+  const unsigned grid = xcd_grid(tp.nseg(), 1, (int64_t)1 << 31);
+  const int npass = (tp.abits + 7) / 8;
+  return with_addr(addr, tp, [&](auto a) {
+    // keys per thread: the fewest that hold the segment
+#define REM_SL(IT)                                                                            \
+  seg_sort_link_kernel<decltype(a), IT, LINK><<<grid, kSortThreads, 0, s>>>(                   \
+      a, wmask, tp.T, tp.C, tp.A, tp.tbits, npass, tp.mode, tp.trunc32 ? 1 : 0, k, tp.nseg(), \
+      src, keys_out)
+    if (tp.T <= 4 * kSortThreads)
+      REM_SL(4);
+    else if (tp.T <= 8 * kSortThreads)
+      REM_SL(8);
+    else
+      REM_SL(kShortItems);
+#undef REM_SL
+    return hipGetLastError();
+  });
+}
+
+bool sort_short_applies(const Tape& tp) {
+  return tp.T >= 1 && tp.T <= kShortT && !tp.wide() && (tp.abits + 7) / 8 <= 4;
+}
+
+bool link_short_applies(const Tape& tp, int64_t k) {
+  return !tp.masked && sort_short_applies(tp) && k >= 1 && tp.n() * k < ((int64_t)1 << 31);
+}
+
+hipError_t link_short(const AddrIn& addr, const Tape& tp, int k, int32_t* src, hipStream_t s) {
+  if (tp.n() == 0) return hipSuccess;
+  if (!link_short_applies(tp, k)) return hipErrorInvalidValue;
+  return seg_sort_short<true>(addr, nullptr, tp, k, src, nullptr, s);
 }
 
 template hipError_t sort_tape<uint32_t>(const AddrIn&, const uint8_t*, const Tape&, uint32_t*,

@@ -305,8 +305,9 @@ def test_stage_timer_reports_each_stage(device):
     from ravel_em import _native as nat
 
     lib = nat.library()
-    w = torch.randint(0, 50, (2, 4000, 4), device=device)
-    p = torch.randn(2, 4000, 4, 8, device=device)
+    # a tape longer than 4096 steps, so the global sort, the resolve and the gather all run
+    w = torch.randint(0, 50, (2, 5000, 4), device=device)
+    p = torch.randn(2, 5000, 4, 8, device=device)
     nat.check(lib.ravel_em_profile_start())
     for _ in range(3):
         causal_last_k_lookup(w, p, address_space=50, k=2)
