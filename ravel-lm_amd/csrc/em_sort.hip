@@ -1336,14 +1336,14 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
 namespace {
 
 constexpr int kShortT = 4096;
-constexpr int kShortItems = kShortT / kSortThreads;
+constexpr int kShortThreads = 1024;
 
-template <typename AS, int ITEMS, bool LINK>
-__global__ __launch_bounds__(kSortThreads) void seg_sort_link_kernel(
+template <typename AS, int ITEMS, bool LINK, int NT>
+__global__ __launch_bounds__(NT) void seg_sort_link_kernel(
     const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int tbits,
     int npass, int mode, int trunc32, int k, int64_t nseg, int32_t* __restrict__ src,
     uint32_t* __restrict__ keys_out) {
-  constexpr int NW = kSortThreads / kWave;
+  constexpr int NW = NT / kWave;
   __shared__ uint32_t wcnt[NW][kRadix];
   __shared__ uint32_t dstart[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
@@ -1375,7 +1375,7 @@ __global__ __launch_bounds__(kSortThreads) void seg_sort_link_kernel(
     const int shift = tbits + 8 * p;
     uint32_t rank[ITEMS];
     uint32_t own;
-    rank_tile<uint32_t, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+    rank_tile<uint32_t, ITEMS, NT>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
     __syncthreads();  // dstart of every digit
     sorted = buf[p & 1];
 #pragma unroll
@@ -1406,10 +1406,10 @@ __global__ __launch_bounds__(kSortThreads) void seg_sort_link_kernel(
     }
     __syncthreads();
   }
-  for (int p = tid; p < n; p += kSortThreads) inv[sorted[p] & tmask] = (uint16_t)p;
+  for (int p = tid; p < n; p += NT) inv[sorted[p] & tmask] = (uint16_t)p;
   __syncthreads();
   const int32_t base = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
-  for (int t = tid; t < n; t += kSortThreads) {
+  for (int t = tid; t < n; t += NT) {
     const int p = inv[t];
     const uint32_t a = sorted[p] >> tbits;
     int32_t* o = src + ((b * T + t) * C + c) * (int64_t)k;
@@ -1451,17 +1451,17 @@ hipError_t seg_sort_short(const AddrIn& addr, const uint8_t* wmask, const Tape& 
   const unsigned grid = xcd_grid(tp.nseg(), 1, (int64_t)1 << 31);
   const int npass = (tp.abits + 7) / 8;
   return with_addr(addr, tp, [&](auto a) {
-    // keys per thread: the fewest that hold the segment
+    // 1024 threads, keys per thread the fewest that hold the segment
 #define REM_SL(IT)                                                                            \
-  seg_sort_link_kernel<decltype(a), IT, LINK><<<grid, kSortThreads, 0, s>>>(                   \
+  seg_sort_link_kernel<decltype(a), IT, LINK, kShortThreads><<<grid, kShortThreads, 0, s>>>(   \
       a, wmask, tp.T, tp.C, tp.A, tp.tbits, npass, tp.mode, tp.trunc32 ? 1 : 0, k, tp.nseg(), \
       src, keys_out)
-    if (tp.T <= 4 * kSortThreads)
-      REM_SL(4);
-    else if (tp.T <= 8 * kSortThreads)
-      REM_SL(8);
+    if (tp.T <= kShortThreads)
+      REM_SL(1);
+    else if (tp.T <= 2 * kShortThreads)
+      REM_SL(2);
     else
-      REM_SL(kShortItems);
+      REM_SL(4);
 #undef REM_SL
     return hipGetLastError();
   });
