@@ -122,6 +122,11 @@ SMALL = [
     (3, 1000, 8, 1024, None, None, False, False, 5),  # batch-row link, ragged time chunks
     (2, 1000, 4, (1 << 23) + 5, None, None, False, False, 3),  # batch-row link over 64-bit keys
     (2, 333, 3, 7, None, None, False, False, 1),  # batch-row link, k = 1, scalar stores
+    (3, 1, 2, 5, None, None, False, False, 2),  # one step: every slot missing
+    (2, 1, 3, 5, None, None, True, True, 1),  # one step, masked, separate reads
+    (1, 4096, 2, 70000, None, None, False, False, 4),  # per-segment LDS sort at its longest, 3 passes
+    (1, 4097, 2, 70000, None, None, True, False, 4),  # one step over it: the global sort, masked
+    (2, 1025, 3, 1 << 16, None, None, True, True, 3),  # short sort, masked, 2 keys per thread
 ]
 
 
