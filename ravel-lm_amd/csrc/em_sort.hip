@@ -251,8 +251,8 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
 // scatter by the low digit and link in the look-back sweep.
 
 constexpr int kPackThreads = 512;
-constexpr int kPackLdsBytes = 33 * 1024;  // keys of one pack tile, [CC][TT + 1]
-constexpr int kHistWords = 4096;          // CC * npass * 256 histogram words
+constexpr int kPackLdsBytes = 33 * 1024;  // keys of one pack tile, [CC][TT + kPackPad]
+constexpr int kHistWords = 4096;          // CC * (histogram passes) * 256 counters
 constexpr int kSweepItems = 16;           // keys per thread of a look-back sweep
 constexpr int kSweepTile = kSortThreads * kSweepItems;
 constexpr uint32_t kFlagA = 1u << 30;     // tile aggregate published
