@@ -10,26 +10,31 @@
 //   out[n, m] = sum_k A[n, k] * W[m, k],   n = b*T + t, k = c*P + p,
 //   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
 //
-// Tiles: a block (8 waves, one block per CU) computes kRows rows x kCols
-// columns over K in chunks of kChunk; wave (g, h) owns rows [64g, 64g+64) and
-// columns [64h, 64h+64).  A chunk's A tile is gathered in 16-byte units (8
-// values; P % 8 == 0 keeps a unit inside one head), W's tile is read row-major,
-// both go to LDS with rows padded to kLds elements (144 bytes: the 16 rows that
-// one MFMA operand read touches land in distinct banks).  A wave runs 4 x 4
-// tiles of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation, rounded once to
-// the payload dtype.  Operand lane layout (checked on the device): A lane l
-// holds row l%16, k (l/16)*8 .. +7; B lane l holds column l%16, the same k; the
-// result lane l holds column l%16, rows (l/16)*4 .. +3.  The epilogue stages
-// the tile in LDS and writes whole 16-byte units of the output rows.
+// Tiles: a block (8 waves, one block per CU) computes kRows rows x 64*CT
+// columns (CT = ceil(M / 64), so every wave has columns to compute) over K in
+// chunks of kChunk; wave (g, h) owns rows [64g, 64g+64) and columns
+// [16*CT*h, 16*CT*(h+1)).  A chunk's A tile is gathered in 16-byte units (8
+// values; P % 8 == 0 keeps a unit inside one head), W's tile is read
+// row-major, both go to LDS with rows padded to kLds elements (144 bytes: the
+// 16 rows that one MFMA operand read touches land in distinct banks).  A wave
+// runs 4 x CT tiles of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation,
+// rounded once to the payload dtype.  Operand lane layout (checked on the
+// device): A lane l holds row l%16, k (l/16)*8 .. +7; B lane l holds column
+// l%16, the same k; the result lane l holds column l%16, rows (l/16)*4 .. +3.
+// The epilogue stages the tile in LDS and writes whole 16-byte units of the
+// output rows.
 //
-// Pipelining: kStages register sets hold the next chunks' units while the
-// current chunk multiplies out of LDS.  Every load is unconditional (a missing
-// or out-of-range unit reads kZeroUnit, a zero in global memory, instead of
-// being skipped or selected) and the chunk loop runs whole rounds of kStages
-// with no branch around its loads, so the compiler's wait counts let the
-// prefetched chunks stay in flight across the barriers (a conditional load or
-// a select on the loaded value makes it wait for every outstanding load).
-// Two stages measured best (three and four: more registers, no gain).
+// Pipelining: two LDS buffers and two register sets.  While a chunk multiplies
+// out of one LDS buffer, the next chunk (loaded into registers two chunks
+// earlier) is stored into the other buffer and the chunk after next is loaded
+// into the freed registers: the LDS stores and the memory latency overlap the
+// MFMA work, and one barrier per chunk separates the buffers.  Every load is
+// unconditional (a missing or out-of-range unit reads kZeroUnit, a zero in
+// global memory, instead of being skipped or selected) and the chunk loop is
+// unrolled by two with no branch around its loads, so the compiler's wait
+// counts let the prefetched chunks stay in flight across the barriers (a
+// conditional load or a select on the loaded value makes it wait for every
+// outstanding load).
 
 #include <type_traits>
 
@@ -39,13 +44,13 @@ namespace rem {
 
 namespace {
 
-constexpr int kThreads = 512;  // 8 waves: 2 row groups x 4 column groups of 64 x 64
+constexpr int kThreads = 512;  // 8 waves: 2 row groups x 4 column groups
 constexpr int kRows = 128;
 constexpr int kSrcLds = 32;  // heads whose sources a block stages in LDS
-constexpr int kCols = 256;
+constexpr int kCols = 256;   // the widest column tile (CT = 4)
 constexpr int kChunk = 64;
 constexpr int kLds = kChunk + 8;
-constexpr int kStages = 2;
+constexpr int kSets = 2;  // register sets of prefetched chunks (even: LDS parity is static)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -75,17 +80,21 @@ __device__ __forceinline__ uint16_t round16(float x) {
 
 __device__ u32x4 kZeroUnit = {0u, 0u, 0u, 0u};  // never written: the unit a missing row reads
 
-template <bool F16, bool SRC_LDS>
+template <bool F16, bool SRC_LDS, int CT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gather_gemm_kernel(
     const uint16_t* __restrict__ payload, const int32_t* __restrict__ src,
     const uint16_t* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
     uint16_t* __restrict__ out) {
-  constexpr int RT = 4;  // 16-row tiles per wave (64 rows)
-  __shared__ __align__(16) uint16_t As[kRows * kLds];
-  __shared__ __align__(16) uint16_t Bs[kCols * kLds];
+  constexpr int RT = 4;             // 16-row tiles per wave (64 rows)
+  constexpr int BC = 64 * CT;       // columns of the block
+  constexpr int AU = kRows * 8 / kThreads;
+  constexpr int BU = BC * 8 / kThreads;
+  static_assert(BU * kThreads == BC * 8, "whole W units per thread");
+  __shared__ __align__(16) uint16_t As[2][kRows * kLds];
+  __shared__ __align__(16) uint16_t Bs[2][BC * kLds];
   __shared__ int32_t Ss[kRows * kSrcLds];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wrow = wave >> 2, wcol = wave & 3;  // 64-row group, 64-column group
+  const int wrow = wave >> 2, wcol = wave & 3;  // 64-row group, column group
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int K = C * P;
   // The block's sources [kRows][C] (one contiguous run) go to LDS once, so a
@@ -95,19 +104,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int i = tid; i < nrow * C; i += kThreads) Ss[i] = src[row0 * C + i];
     __syncthreads();
   }
-  f32x4_t acc[RT][4];
+  f32x4_t acc[RT][CT];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const bool wave_live = wcol * 64 < M;  // columns past M are padding
-  // The next chunk's tiles are loaded into registers while the current chunk
-  // multiplies out of LDS.
-  constexpr int AU = kRows * 8 / kThreads;
-  constexpr int BU = kCols * 8 / kThreads;
-  u32x4 av[kStages][AU], bv[kStages][BU];
+    for (int j = 0; j < CT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4 av[kSets][AU], bv[kSets][BU];
   const u32x4* zero = &kZeroUnit;
-  auto load_chunk = [&](int k0, u32x4 (&a)[AU], u32x4 (&bb)[BU]) {
+  auto load_chunk = [&](int ch, u32x4 (&a)[AU], u32x4 (&bb)[BU]) {
+    const int k0 = ch * kChunk;
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
       const int u = tid + kThreads * q;
@@ -131,65 +136,74 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       bb[q] = *(in ? (const u32x4*)(W + (int64_t)m * K + k) : zero);
     }
   };
-  // Chunks rounded up to whole rounds of kStages (chunks past K read zero
-  // units), so the loop body is straight-line: every stage issues its loads.
+  auto store_chunk = [&](int buf, const u32x4 (&a)[AU], const u32x4 (&bb)[BU]) {
+#pragma unroll
+    for (int q = 0; q < AU; ++q) {
+      const int u = tid + kThreads * q;
+      *(u32x4*)&As[buf][(u >> 3) * kLds + (u & 7) * 8] = a[q];
+    }
+#pragma unroll
+    for (int q = 0; q < BU; ++q) {
+      const int u = tid + kThreads * q;
+      *(u32x4*)&Bs[buf][(u >> 3) * kLds + (u & 7) * 8] = bb[q];
+    }
+  };
+  auto multiply = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < kChunk / 32; ++ks) {
+      const int kk = ks * 32 + (lane >> 4) * 8;
+      u32x4 b[CT];
+#pragma unroll
+      for (int j = 0; j < CT; ++j)
+        b[j] = *(const u32x4*)&Bs[buf][(wcol * 16 * CT + j * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        const u32x4 a = *(const u32x4*)&As[buf][(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
+      }
+    }
+  };
+  // Chunks rounded up to whole rounds of kSets (chunks past K read zero
+  // units), so the loop body is straight-line; loads past the last chunk
+  // re-read it.  Chunk c multiplies out of LDS buffer c % 2 while chunk c + 1
+  // waits in register set (c + 1) % kSets, loaded kSets - 1 chunks earlier.
   const int nch = (K + kChunk - 1) / kChunk;
-  const int nchp = (nch + kStages - 1) / kStages * kStages;
+  const int nchp = (nch + kSets - 1) / kSets * kSets;
+  auto clampc = [&](int ch) { return ch < nchp ? ch : nchp - 1; };
 #pragma unroll
-  for (int st = 0; st < kStages; ++st) load_chunk(st * kChunk, av[st], bv[st]);
-  for (int c0 = 0; c0 < nchp; c0 += kStages) {
+  for (int st = 0; st < kSets; ++st) load_chunk(clampc(st), av[st], bv[st]);
+  store_chunk(0, av[0], bv[0]);
+  __syncthreads();
+  for (int c0 = 0; c0 < nchp; c0 += kSets) {
 #pragma unroll
-    for (int st = 0; st < kStages; ++st) {
-      const int ch = c0 + st;
-#pragma unroll
-      for (int q = 0; q < AU; ++q) {
-        const int u = tid + kThreads * q;
-        *(u32x4*)&As[(u >> 3) * kLds + (u & 7) * 8] = av[st][q];
-      }
-#pragma unroll
-      for (int q = 0; q < BU; ++q) {
-        const int u = tid + kThreads * q;
-        *(u32x4*)&Bs[(u >> 3) * kLds + (u & 7) * 8] = bv[st][q];
-      }
-      __syncthreads();
-      // Always issued (past the end it re-reads the last chunk, unused).
-      load_chunk((ch + kStages < nchp ? ch + kStages : nchp - 1) * kChunk, av[st], bv[st]);
-      if (wave_live) {
-#pragma unroll
-        for (int ks = 0; ks < kChunk / 32; ++ks) {
-          const int kk = ks * 32 + (lane >> 4) * 8;
-          u32x4 b[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            b[j] = *(const u32x4*)&Bs[(wcol * 64 + j * 16 + (lane & 15)) * kLds + kk];
-#pragma unroll
-          for (int i = 0; i < RT; ++i) {
-            const u32x4 a = *(const u32x4*)&As[(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
-          }
-        }
-      }
+    for (int st = 0; st < kSets; ++st) {
+      // set st (chunk c0 + st) went to LDS in the previous step: reload it early
+      load_chunk(clampc(c0 + st + kSets), av[st], bv[st]);
+      multiply(st & 1);
+      __builtin_amdgcn_sched_barrier(0);  // the MFMAs issue before the stores wait
+      store_chunk((st + 1) & 1, av[(st + 1) % kSets], bv[(st + 1) % kSets]);
       __syncthreads();
     }
   }
-  // Epilogue: round to 16 bits and stage the tile in the (now free) B buffer,
-  // kRows/2 rows at a time (padded rows of kCols + 8), then write 16-byte units.
-  uint16_t* Cs = Bs;
-  constexpr int CSTRIDE = kCols + 8;
-  static_assert(kRows / 2 * CSTRIDE <= kCols * kLds, "epilogue half-tile must fit the B buffer");
+  // Epilogue: round to 16 bits and stage the tile in the (now free) B
+  // buffers, kRows/2 rows at a time (padded rows of BC + 8), then write
+  // 16-byte units.
+  uint16_t* Cs = &Bs[0][0];
+  constexpr int CSTRIDE = BC + 8;
+  static_assert(kRows / 2 * CSTRIDE <= 2 * BC * kLds, "epilogue half-tile must fit the B buffers");
   // Half h holds the rows of row group h.
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    if (wave_live && wrow == half) {
+    if (wrow == half) {
 #pragma unroll
       for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < CT; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = i * 16 + (lane >> 4) * 4 + e;
-            const int col = wcol * 64 + j * 16 + (lane & 15);
+            const int col = wcol * 16 * CT + j * 16 + (lane & 15);
             Cs[r * CSTRIDE + col] = round16<F16>(acc[i][j][e]);
           }
     }
@@ -219,10 +233,20 @@ hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, i
   if (blocks > INT32_MAX || C * P > INT32_MAX) return hipErrorInvalidValue;
   const int64_t nsrc = NR * C;
   const FastDiv byP = make_fastdiv((uint32_t)P);
+  const int ct = (int)((M + 63) / 64);  // 16-column tiles per wave: ceil(M / 64)
   auto go = [&](auto f16, auto src_lds) {
-    gather_gemm_kernel<decltype(f16)::value, decltype(src_lds)::value>
-        <<<(unsigned)blocks, kThreads, 0, s>>>((const uint16_t*)payload, src, (const uint16_t*)W, NR,
-                                              (int)C, (int)P, byP, (int)M, nsrc, (uint16_t*)out);
+    constexpr bool F = decltype(f16)::value, SL = decltype(src_lds)::value;
+#define REM_GG(CT)                                                                              \
+  gather_gemm_kernel<F, SL, CT><<<(unsigned)blocks, kThreads, 0, s>>>(                           \
+      (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, byP, (int)M, nsrc, \
+      (uint16_t*)out)
+    switch (ct) {
+      case 1: REM_GG(1); break;
+      case 2: REM_GG(2); break;
+      case 3: REM_GG(3); break;
+      default: REM_GG(4); break;
+    }
+#undef REM_GG
   };
   using T_ = std::true_type;
   using F_ = std::false_type;

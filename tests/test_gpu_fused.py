@@ -42,6 +42,9 @@ CASES = [
     (2, 130, 4, 16, 256, 13, torch.float16, False),     # f16, M = 256 (all four column waves)
     (1, 1000, 2, 32, 64, 5, torch.bfloat16, True),      # separate reads
     (3, 45, 1, 128, 120, 7, torch.bfloat16, False),     # one head, K = 128
+    (2, 200, 8, 64, 128, 31, torch.bfloat16, False),    # two column tiles per wave
+    (1, 150, 5, 24, 200, 9, torch.float16, False),      # four column tiles, M not a multiple of 64
+    (1, 90, 2, 8, 40, 3, torch.bfloat16, False),        # one column tile, K = 16
 ]
 
 
