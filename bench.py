@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--suite", action="store_true",
                     help="time every BASELINE config (cfg1-cfg5), one JSON line per op, instead of the headline")
     ap.add_argument("--suite-parts", nargs="+", default=None, metavar="PART",
-                    help="with --suite: only these parts (tapes, addresses, decode)")
+                    help="with --suite: only these parts (tapes, addresses, decode, fused)")
     return ap.parse_args()
 
 

@@ -288,7 +288,40 @@ def decode_address_lines(dev: torch.device, cache: RavelLayerCache, w, steps: in
     return lines
 
 
-PARTS = ("tapes", "addresses", "decode")
+def fused_lines(dev: torch.device, iters: int) -> List[dict]:
+    """The latest-1 lookup fused into the fuse layer's linear map on the cfg4 tape
+    (`fused_latest1_linear`), against the lookup followed by torch's matmul
+    (hipBLASLt), for M = 64, 192, 256 output columns of a bf16 W [M, C*D]
+    (ravel_lm/triton_memory.py:378-426 is the reference's fused arm).  Bytes:
+    addresses + payload rows read once + W + out; the unfused form also writes
+    and reads the [B*T, C*D] lookup."""
+    from .fused import fused_latest1_linear
+    lines: List[dict] = []
+    w = workloads.cfg4(dev)
+    B, T, C, D = w.shape
+    for M in (64, 192, 256):
+        g = torch.Generator(device=dev).manual_seed(M)
+        W = (torch.randn(M, C * D, generator=g, device=dev) / (C * D) ** 0.5).to(torch.bfloat16)
+
+        def fused():
+            return fused_latest1_linear(w.write, w.payload, None, W, address_space=w.address_space)
+
+        def unfused():
+            v, _ = causal_last_k_lookup(w.write, w.payload, address_space=w.address_space, k=1)
+            return torch.matmul(v.reshape(B * T, C * D), W.t())
+
+        nbytes = w.write.numel() * 8 + w.payload.numel() * 2 + W.numel() * 2 + B * T * M * 2
+        flops = 2 * B * T * C * D * M
+        for form, fn in (("fused", fused), ("lookup_then_matmul", unfused)):
+            us = statistics.median(time_calls(fn, iters=iters))
+            lines.append(_line("cfg4", f"latest1_linear_M{M}_{form}", us, nbytes, B * T, M=M,
+                               TFLOPs=round(flops / (us * 1e-6) / 1e12, 1)))
+    del w
+    torch.cuda.empty_cache()
+    return lines
+
+
+PARTS = ("tapes", "addresses", "decode", "fused")
 
 
 def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
@@ -326,11 +359,14 @@ def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
     for line in decode_lines(dev, cpu=cpu) if "decode" in parts else []:
         print(json.dumps(line), flush=True)
         lines.append(line)
+    for line in fused_lines(dev, iters) if "fused" in parts else []:
+        print(json.dumps(line), flush=True)
+        lines.append(line)
     return lines
 
 
 def main(argv=None) -> None:
-    """``python -m ravel_em.suite [part ...]`` with parts among tapes, addresses, decode."""
+    """``python -m ravel_em.suite [part ...]`` with parts among tapes, addresses, decode, fused."""
     if not torch.cuda.is_available():
         sys.exit("the suite needs a ROCm GPU")
     parts = (argv if argv is not None else sys.argv[1:]) or PARTS
