@@ -118,3 +118,53 @@ def test_sum_matches_reference_outputs(device, case):
     rtol, atol = TOL[p.dtype]
     lim = golden_sums.reference_bound(p, truth, m) + rtol * truth.abs() + atol * scale
     assert ((out.double() - ref.double()).abs() <= lim).all()
+
+
+# Separate reads without a write mask: rows of 1 to 8 16-byte units in every
+# payload dtype, over the short-tape sort's sizes and one step past them.
+SEP_ROWS = [(torch.float32, 4), (torch.float32, 16), (torch.bfloat16, 64), (torch.float16, 8),
+            (torch.float64, 2), (torch.float64, 16)]
+SEP_SHAPES = [
+    (2, 1, 3, 5),      # one step: every read sees nothing
+    (2, 17, 3, 11),
+    (3, 1000, 2, 7),   # long runs spanning every walker of a segment
+    (1, 4096, 2, 1),   # one address; the longest short tape
+    (2, 4096, 2, 4096),
+    (2, 1025, 1, 300),
+    (1, 2049, 3, 40),
+    (1, 4097, 1, 50),  # one step over: the global sort
+]
+
+
+@pytest.mark.parametrize("shape", SEP_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype,D", SEP_ROWS, ids=lambda x: str(x).replace("torch.", ""))
+def test_sum_separate_reads(device, shape, dtype, D):
+    B, T, C, A = shape
+    print(f"[separate-read sum] {shape} {dtype} D={D}", flush=True)
+    g = torch.Generator().manual_seed(T * 7 + D)
+    w = torch.randint(-A, 2 * A, (B, T, C), generator=g)  # out-of-range ids wrap (Python %)
+    r = torch.randint(-A, 2 * A, (B, T, C), generator=g)
+    p = torch.randn(B, T, C, D, generator=g).to(dtype)
+    check_sum(w.to(device), p.to(device), r.to(device), A=A)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 4)])
+def test_sum_reads_equal_to_writes_match_direct(device, dtype, D):
+    """The same addresses passed as separate reads give the direct sum (integer
+    payloads, so the two paths' different summation orders agree exactly)."""
+    g = torch.Generator().manual_seed(11)
+    w = torch.randint(0, 9, (2, 3000, 4), generator=g).to(device)
+    p = torch.randint(-3, 4, (2, 3000, 4, D), generator=g).to(dtype).to(device)
+    direct, dmask = causal_sum_lookup(w, p, address_space=9)
+    sep, smask = causal_sum_lookup(w, p, w.clone(), address_space=9)
+    assert torch.equal(dmask, smask) and torch.equal(direct, sep)
+
+
+def test_sum_reads_disjoint_from_writes(device):
+    g = torch.Generator().manual_seed(12)
+    w = torch.randint(0, 50, (2, 2000, 3), generator=g).to(device)
+    r = torch.randint(50, 100, (2, 2000, 3), generator=g).to(device)
+    p = torch.randn(2, 2000, 3, 8, generator=g).to(device)
+    out, mask = causal_sum_lookup(w, p, r, address_space=100)
+    assert not mask.any() and not out.any()
+
