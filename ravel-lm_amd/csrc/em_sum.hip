@@ -341,6 +341,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   __shared__ uint8_t hs[NWMAX];
   __shared__ Acc tl[kWalkThreads * CPU];  // [walker][column]
   __shared__ uint32_t s_part;
+  __shared__ uint8_t s_next;  // the position after the part starts a run (or the segment ends)
+  // Exclusive forward sums never add the last row of a run to any output:
+  // those rows are not loaded (on a uniform tape most runs are one record).
+  constexpr bool SKIP_LAST = !INCL && !REV;
   const int tid = threadIdx.x;
   const int64_t seg = blockIdx.x / nparts;
   if (tid == 0) s_part = (uint32_t)atomicAdd((unsigned long long*)&tickets[seg], 1ull);
@@ -372,7 +376,12 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     }
     st[i] = start ? 1 : 0;
   }
+  if (SKIP_LAST && tid == 0)
+    s_next = (p0 + n >= T || (sk[p0 + n] >> tbits) != (kk[n - 1] >> tbits)) ? 1 : 0;
   __syncthreads();
+  auto needed = [&](int i) -> bool {  // row i feeds a later output of its run
+    return !SKIP_LAST || ((i + 1 < n) ? st[i + 1] == 0 : s_next == 0);
+  };
   const int NW = kWalkThreads / G;
   const int w = tid / G, v = tid - (tid / G) * G;
   const int len = (n + NW - 1) / NW;
@@ -403,7 +412,7 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 #pragma unroll
     for (int m = 0; m < kWalkBatch; ++m) {
       const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = inv[(int64_t)irow(i) * G + v];
+      x[m] = needed(i) ? inv[(int64_t)irow(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int m = 0; m < kWalkBatch; ++m)
@@ -452,7 +461,7 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 #pragma unroll
     for (int m = 0; m < kWalkBatch; ++m) {
       const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = inv[(int64_t)irow(i) * G + v];
+      x[m] = needed(i) ? inv[(int64_t)irow(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
     }
     OutV* ou = (OutV*)out + v;  // unit v of row r is ou[r * G]
 #pragma unroll
