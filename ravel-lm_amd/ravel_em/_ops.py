@@ -21,11 +21,21 @@ def _call(fn, *args) -> None:
     nat.check(fn(*args))
 
 
+def eager(*tensors: Optional[Tensor]) -> bool:
+    """True when a call may run an op's implementation directly instead of
+    through the dispatcher: nothing is tracing (no torch.compile) and every
+    tensor is a plain tensor (no fake, meta-programming or other subclass).
+    The callers also require that no autograd graph is recorded.  The
+    dispatcher costs several microseconds a call, which short tapes notice."""
+    if torch.compiler.is_compiling():
+        return False
+    return all(t is None or type(t) is torch.Tensor for t in tensors)
+
+
 # ------------------------------------------------------------- latest-k --
 
 
-@torch.library.custom_op("ravel_em::latest_k", mutates_args=())
-def latest_k(
+def latest_k_impl(
     write_addresses: Tensor,
     payloads: Tensor,
     read_addresses: Optional[Tensor],
@@ -34,6 +44,7 @@ def latest_k(
     k: int,
     want_src: bool,
 ) -> Tuple[Tensor, Tensor, Tensor]:
+    """The body of ravel_em::latest_k (also called directly, see eager)."""
     lib = nat.library()
     B, T, C = write_addresses.shape
     D = payloads.shape[-1]
@@ -54,6 +65,20 @@ def latest_k(
         nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
     )
     return values, mask, src
+
+
+@torch.library.custom_op("ravel_em::latest_k", mutates_args=())
+def latest_k(
+    write_addresses: Tensor,
+    payloads: Tensor,
+    read_addresses: Optional[Tensor],
+    write_mask: Optional[Tensor],
+    address_space: int,
+    k: int,
+    want_src: bool,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    return latest_k_impl(write_addresses, payloads, read_addresses, write_mask, address_space, k,
+                         want_src)
 
 
 @latest_k.register_fake
@@ -114,14 +139,14 @@ latest_k.register_autograd(_latest_k_grad, setup_context=_latest_k_setup)
 # -------------------------------------------------------------- seg-sum --
 
 
-@torch.library.custom_op("ravel_em::seg_sum", mutates_args=())
-def seg_sum(
+def seg_sum_impl(
     write_addresses: Tensor,
     payloads: Tensor,
     read_addresses: Optional[Tensor],
     write_mask: Optional[Tensor],
     address_space: int,
 ) -> Tuple[Tensor, Tensor]:
+    """The body of ravel_em::seg_sum (also called directly, see eager)."""
     lib = nat.library()
     B, T, C = write_addresses.shape
     D = payloads.shape[-1]
@@ -140,6 +165,17 @@ def seg_sum(
         nat.ptr(out), nat.ptr(mask), nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
     )
     return out, mask
+
+
+@torch.library.custom_op("ravel_em::seg_sum", mutates_args=())
+def seg_sum(
+    write_addresses: Tensor,
+    payloads: Tensor,
+    read_addresses: Optional[Tensor],
+    write_mask: Optional[Tensor],
+    address_space: int,
+) -> Tuple[Tensor, Tensor]:
+    return seg_sum_impl(write_addresses, payloads, read_addresses, write_mask, address_space)
 
 
 @seg_sum.register_fake

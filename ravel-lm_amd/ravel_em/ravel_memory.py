@@ -121,7 +121,9 @@ def causal_last_k_lookup(
     w, r = _prepare(write_addresses, None if same else read_addresses, key_dtype)
     m = None if write_mask is None else write_mask.bool().contiguous()
     want_src = torch.is_grad_enabled() and payloads.requires_grad
-    values, mask, _ = _ops.latest_k(w, payloads.contiguous(), r, m, int(address_space), int(k), want_src)
+    p = payloads.contiguous()
+    op = _ops.latest_k_impl if not want_src and _ops.eager(w, p, r, m) else _ops.latest_k
+    values, mask, _ = op(w, p, r, m, int(address_space), int(k), want_src)
     return values, mask
 
 
@@ -201,7 +203,10 @@ def causal_sum_lookup(
     key_dtype = _composite_key_dtype(B, T, C, address_space)
     w, r = _prepare(write_addresses, None if same else read_addresses, key_dtype)
     m = None if write_mask is None else write_mask.bool().contiguous()
-    return _ops.seg_sum(w, payloads.contiguous(), r, m, int(address_space))
+    p = payloads.contiguous()
+    graph = torch.is_grad_enabled() and p.requires_grad
+    op = _ops.seg_sum_impl if not graph and _ops.eager(w, p, r, m) else _ops.seg_sum
+    return op(w, p, r, m, int(address_space))
 
 
 def sort_order(

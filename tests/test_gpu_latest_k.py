@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle
-from ravel_em import causal_last_k_lookup, causal_last_k_sources, sort_order, workloads
+from ravel_em import causal_last_k_lookup, causal_last_k_sources, causal_sum_lookup, sort_order, workloads
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -393,3 +393,19 @@ def test_multi_piece_buckets(device, case):
     w = _hot_case(name, T, A)
     p = torch.randn(*w.shape, 8).to(torch.bfloat16)
     check_against_oracle(w.to(device), p.to(device), A=A, k=1)
+
+
+def test_eager_fast_path_matches_the_registered_op(device):
+    """The public calls without autograd run the ops' bodies directly; the
+    registered ops (the autograd and torch.compile route) give the same bits."""
+    from ravel_em import _ops
+
+    g = torch.Generator().manual_seed(21)
+    w = torch.randint(0, 40, (2, 300, 3), generator=g).to(device)
+    p = torch.randn(2, 300, 3, 8, generator=g).to(device)
+    vals, mask = causal_last_k_lookup(w, p, address_space=40, k=3)
+    v2, m2, _ = _ops.latest_k(w, p, None, None, 40, 3, False)
+    assert torch.equal(vals, v2) and torch.equal(mask, m2)
+    s, sm = causal_sum_lookup(w, p, address_space=40)
+    s2, sm2 = _ops.seg_sum(w, p, None, None, 40)
+    assert torch.equal(s, s2) and torch.equal(sm, sm2)

@@ -90,3 +90,18 @@ def test_fused_latest1_linear_errors_match_reference():
         fused_latest1_linear(w, p, None, torch.zeros(5, 31), address_space=9)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         fused_latest1_linear(w, p, None, torch.zeros(5, 32), address_space=9)
+
+
+def test_eager_fast_path_only_for_plain_tensors_outside_compile():
+    """Plain tensors outside torch.compile may skip the dispatcher; a tensor
+    subclass (as torch.compile's fake tensors are) or tracing keeps the op."""
+    from ravel_em import _ops
+
+    class Sub(torch.Tensor):
+        pass
+
+    t = torch.zeros(2, 3, 4)
+    assert _ops.eager(t, None, t)
+    assert not _ops.eager(t, t.as_subclass(Sub))
+    compiled = torch.compile(lambda x: x + int(_ops.eager(x)), backend="eager", fullgraph=True)
+    assert compiled(torch.zeros(1)).item() == 0.0
