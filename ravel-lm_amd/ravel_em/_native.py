@@ -129,7 +129,16 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+# torch's raw current-stream accessor (the one its generated kernels' launchers
+# call) skips building a Stream object on every call; the public route stays as
+# the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """Handle of torch's current stream on t's device (the launch stream)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

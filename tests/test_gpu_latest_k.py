@@ -409,3 +409,19 @@ def test_eager_fast_path_matches_the_registered_op(device):
     s, sm = causal_sum_lookup(w, p, address_space=40)
     s2, sm2 = _ops.seg_sum(w, p, None, None, 40)
     assert torch.equal(s, s2) and torch.equal(sm, sm2)
+
+
+def test_launch_stream_is_torch_current_stream(device):
+    from ravel_em import _native as nat
+
+    t = torch.zeros(4, device=device)
+    assert nat.stream_of(t) == torch.cuda.current_stream(device).cuda_stream
+    side = torch.cuda.Stream(device)
+    with torch.cuda.stream(side):
+        assert nat.stream_of(t) == side.cuda_stream
+        w = torch.randint(0, 9, (1, 64, 2), device=device)
+        p = torch.randn(1, 64, 2, 4, device=device)
+        vals, mask = causal_last_k_lookup(w, p, address_space=9)
+    side.synchronize()
+    ref, rmask = causal_last_k_lookup(w, p, address_space=9)
+    assert torch.equal(vals, ref) and torch.equal(mask, rmask)
