@@ -95,3 +95,27 @@ def test_cache_step_replays_match_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(vals, ev) and torch.equal(mask, em)
         assert torch.equal(cache.values, eager.values) and torch.equal(cache.filled, eager.filled)
+
+
+def test_torch_compile_traces_through_the_lookups(device):
+    """fullgraph tracing goes through the registered ops (fake implementations
+    and autograd formulas); results and gradients equal the eager calls."""
+    g = torch.Generator().manual_seed(9)
+    w = torch.randint(0, 30, (2, 200, 3), generator=g).to(device)
+    p = torch.randn(2, 200, 3, 8, generator=g).to(device)
+
+    def f(w, p):
+        vals, mask = causal_last_k_lookup(w, p, address_space=30, k=2)
+        s, smask = causal_sum_lookup(w, p, address_space=30)
+        return vals.sum(dim=3) * mask.any(dim=3, keepdim=True) + s * smask.unsqueeze(-1)
+
+    compiled = torch.compile(f, backend="aot_eager", fullgraph=True)
+    pe = p.clone().requires_grad_(True)
+    pc = p.clone().requires_grad_(True)
+    want = f(w, pe)
+    got = compiled(w, pc)
+    assert torch.equal(got, want)
+    weights = torch.randn_like(want)
+    (want * weights).sum().backward()
+    (got * weights).sum().backward()
+    assert torch.allclose(pc.grad, pe.grad, rtol=1e-6, atol=1e-6)
