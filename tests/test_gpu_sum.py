@@ -168,3 +168,17 @@ def test_sum_reads_disjoint_from_writes(device):
     out, mask = causal_sum_lookup(w, p, r, address_space=100)
     assert not mask.any() and not out.any()
 
+
+
+@pytest.mark.parametrize("sep", [False, True])
+def test_sum_unaligned_payload(device, sep):
+    """A payload view 2 bytes into its storage (16-byte rows that are not
+    16-byte aligned) takes the chunk kernels instead of the walker."""
+    g = torch.Generator().manual_seed(31)
+    B, T, C, D, A = 2, 700, 3, 8, 13
+    w = torch.randint(0, A, (B, T, C), generator=g)
+    r = torch.randint(0, A, (B, T, C), generator=g) if sep else None
+    base = torch.randn(B * T * C * D + 1, generator=g).to(torch.bfloat16)
+    p = base.to(device)[1:].view(B, T, C, D)
+    assert p.data_ptr() % 16 != 0 and p.is_contiguous()
+    check_sum(w.to(device), p, None if r is None else r.to(device), A=A)
