@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X event-memory operator.
 
-Metric: event-memory prefill tokens/sec at 1 GPU + achieved HBM
-GB/s (% of peak).  Workload: BASELINE cfg4, the latest-1 forward of
+Metric: event-memory prefill tokens/sec at 1 GPU + achieved HBM GB/s (% of
+peak).  Workload: benchmark configuration cfg4, the latest-1 forward of
 causal_last_k_lookup at B=4, T=65536, H=16 heads, A=65536 addresses, D=64 bf16
 payload (N = 4,194,304 records), synthetic seeded inputs resident in HBM.
 
@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--suite", action="store_true",
-                    help="time every BASELINE config (cfg1-cfg5), one JSON line per op, instead of the headline")
+                    help="time every benchmark config (cfg1-cfg5), one JSON line per op, instead of the headline")
     ap.add_argument("--suite-parts", nargs="+", default=None, metavar="PART",
                     help="with --suite: only these parts (tapes, addresses, decode, fused)")
     return ap.parse_args()

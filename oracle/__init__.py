@@ -8,7 +8,7 @@ ravel-lm_amd/ravel_em never touches it.
 Three independent restatements of the reference operator
 (ravel_lm/ravel_memory.py):
   * ravel_oracle.c (wrapped here): per-stream history replay in plain C,
-    sized for full BASELINE shapes;
+    sized for the full benchmark shapes;
   * torch_ref.py: the reference's own algorithm (composite keys, torch.sort,
     searchsorted, gathers, global cumsum) restated on the CPU; it is also the
     CPU baseline timed by bench.py;

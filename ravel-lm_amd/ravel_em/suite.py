@@ -1,4 +1,4 @@
-"""Device timing of every BASELINE configuration (cfg1-cfg5) on one GPU.
+"""Device timing of every benchmark configuration (cfg1-cfg5) on one GPU.
 
 ``python -m ravel_em.suite`` (or ``python bench.py --suite``) prints one JSON
 line per measurement:

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the five BASELINE configurations.
+"""Seeded synthetic inputs for the five benchmark configurations (cfg1-cfg5).
 
 Inputs are drawn with a ``torch.Generator`` on the target device (fast at the
 large configs; deterministic per seed and device type).  Addresses are int64,

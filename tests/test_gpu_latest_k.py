@@ -248,7 +248,7 @@ def test_empty_tape(device):
     assert vals.shape == (0, 8, 3, 2, 4) and mask.shape == (0, 8, 3, 2)
 
 
-# ------------------------------------------------- BASELINE configurations --
+# ---------------------------------------------- benchmark configurations --
 
 
 @pytest.mark.parametrize("name", ["cfg1", "cfg1b", "cfg2_f32", "cfg2_bf16", "cfg3", "cfg4", "cfg4_adv"])
