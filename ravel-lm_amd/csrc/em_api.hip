@@ -253,7 +253,7 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
     stage_end(kStageSort, s);
     if (e != hipSuccess) return hip_fail(e, "sort");
     stage_begin(kStageGather, s);
-    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s, k == 1);
     stage_end(kStageGather, s);
     if (e != hipSuccess) return hip_fail(e, "gather");
     return RAVEL_EM_OK;
@@ -276,7 +276,9 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   stage_end(kStageResolve, s);
   if (e != hipSuccess) return hip_fail(e, "resolve");
   stage_begin(kStageGather, s);
-  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s);
+  // reads = writes and k == 1: every record is the source of at most one slot
+  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s,
+                  link && k == 1);
   stage_end(kStageGather, s);
   if (e != hipSuccess) return hip_fail(e, "gather");
   return RAVEL_EM_OK;

@@ -241,9 +241,11 @@ hipError_t write_addresses(const AddrIn& a, const Tape& tp, int out_dtype, void*
 hipError_t compact_addresses(const AddrIn& a, const Tape& tp, void* buf, AddrIn* out,
                              hipStream_t s);
 
-// out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0
+// out[row] = src[row] in [0, nsrc) ? rows[src[row]] : 0 ; mask[row] = src[row] >= 0.
+// once: no source row is named twice (its loads may skip the cache).
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
-                       int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s);
+                       int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s,
+                       bool once = false);
 // out[n, m] = sum_k A[n, k] W[m, k] with A gathered through record-major k == 1
 // sources (n = b*T + t, k = c*P + p); 16-bit payloads (bf16/f16), W [M][C*P] of
 // the same dtype, out [NR][M].  gather_gemm_apply says whether the MFMA kernel

@@ -324,7 +324,11 @@ __global__ __launch_bounds__(256) void search_lds_kernel(
 // the output writes over all eight L2s.
 constexpr int kIlp = 2;
 
-template <typename V, int SHIFT>
+// NT: every source row is read at most once (latest-1 with reads = writes:
+// a record is the predecessor of at most one other), so the row loads are
+// non-temporal and leave L2 to the sources and the output stream.  Rows that
+// several slots read (k > 1, separate reads) keep cached loads.
+template <typename V, int SHIFT, bool NT = false>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ rows,
                                                          const int32_t* __restrict__ src,
                                                          int64_t nrows, int upr, int64_t nsrc,
@@ -354,7 +358,11 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
 #pragma unroll
     for (int i = 0; i < kIlp; ++i) {
       if (s[i] >= 0 && s[i] < nsrc) {
-        val[i] = rows[(int64_t)s[i] * upr + v[i]];
+        const V* pr = &rows[(int64_t)s[i] * upr + v[i]];
+        if constexpr (NT)
+          val[i] = __builtin_nontemporal_load(pr);
+        else
+          val[i] = *pr;
       } else {
         val[i] = V{};
       }
@@ -370,13 +378,13 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
   }
 }
 
-template <typename V>
+template <typename V, bool NT = false>
 hipError_t gather_typed(const void* rows, const int32_t* src, int64_t nrows, int upr, int64_t nsrc,
                         void* out, uint8_t* mask, hipStream_t s) {
   const unsigned grid = xcd_grid(nrows * upr, 256 * kIlp);
   const V* r = (const V*)rows;
   V* o = (V*)out;
-#define REM_G(SH) gather_rows_kernel<V, SH><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask)
+#define REM_G(SH) gather_rows_kernel<V, SH, NT><<<grid, 256, 0, s>>>(r, src, nrows, upr, nsrc, o, mask)
   switch (upr) {
     case 1: REM_G(0); break;
     case 2: REM_G(1); break;
@@ -761,12 +769,14 @@ hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32
 }
 
 hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64_t nrows,
-                       int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s) {
+                       int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s, bool once) {
   if (nrows == 0) return hipSuccess;
   // The widest unit that the row size and both base addresses allow.
   const uintptr_t align = (uintptr_t)rows | (uintptr_t)out | (uintptr_t)row_bytes;
   if ((align & 15) == 0)
-    return gather_typed<u32x4>(rows, src, nrows, (int)(row_bytes / 16), nsrc, out, mask, s);
+    return once ? gather_typed<u32x4, true>(rows, src, nrows, (int)(row_bytes / 16), nsrc, out,
+                                            mask, s)
+                : gather_typed<u32x4>(rows, src, nrows, (int)(row_bytes / 16), nsrc, out, mask, s);
   if ((align & 7) == 0)
     return gather_typed<u32x2>(rows, src, nrows, (int)(row_bytes / 8), nsrc, out, mask, s);
   if ((align & 3) == 0)
