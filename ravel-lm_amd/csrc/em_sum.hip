@@ -453,7 +453,9 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     }
   }
   __syncthreads();
-  // 4. walk with the carry-in and write the sums
+  // 4. walk with the carry-in and write the sums.  Every row is loaded and
+  // every sum stored once here (the tails of step 2 are short), so both go
+  // non-temporal and leave L2 to the keys.
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
   for (int i0 = rs; i0 < re; i0 += kWalkBatch) {
@@ -461,7 +463,8 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 #pragma unroll
     for (int m = 0; m < kWalkBatch; ++m) {
       const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = needed(i) ? inv[(int64_t)irow(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
+      x[m] = needed(i) ? __builtin_nontemporal_load(&inv[(int64_t)irow(i) * G + v])
+                        : u32x4{0u, 0u, 0u, 0u};
     }
     OutV* ou = (OutV*)out + v;  // unit v of row r is ou[r * G]
 #pragma unroll
@@ -474,9 +477,9 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
           for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
         }
         const int64_t orw = orow(i);
-        if (!INCL) ou[orw * G] = pack_unit<XOut, StoreF, Acc, CPU>(acc);
+        if (!INCL) __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[orw * G]);
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
-        if (INCL) ou[orw * G] = pack_unit<XOut, StoreF, Acc, CPU>(acc);
+        if (INCL) __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[orw * G]);
         if (WMASK && v == 0) omask[orw] = start ? 0 : 1;
       }
     }
