@@ -280,12 +280,13 @@ __global__ __launch_bounds__(256) void prefill_kept_kernel(
       if (e >= k) continue;
       const int64_t t = (int64_t)(u & tmask);
       dst[j] = ((seg * A + (int64_t)a) * k + e) * upr + v;
-      val[j] = payload[((b * T + t) * C + c) * upr + v];
+      // each kept row is read once and its cache row written once: non-temporal
+      val[j] = __builtin_nontemporal_load(&payload[((b * T + t) * C + c) * upr + v]);
     }
 #pragma unroll
     for (int j = 0; j < kPrefillBatch; ++j) {
       if (dst[j] < 0) continue;
-      values[dst[j]] = val[j];
+      __builtin_nontemporal_store(val[j], &values[dst[j]]);
       if (dst[j] % upr == 0) filled[dst[j] / upr] = 1;
     }
   }

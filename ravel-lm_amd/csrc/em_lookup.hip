@@ -627,7 +627,8 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ p, int6
   const uint32_t w = 0x01010101u * v;
   const u32x4 vv = {w, w, w, w};
   u32x4* q = (u32x4*)(p + head);
-  for (int64_t i = tid; i < body; i += stride) q[i] = vv;
+  // streaming stores: a fill is never read back by this kernel
+  for (int64_t i = tid; i < body; i += stride) __builtin_nontemporal_store(vv, &q[i]);
   const int64_t rest = n - body * 16;  // head + tail bytes
   for (int64_t i = tid; i < rest; i += stride) p[i < head ? i : i + body * 16] = v;
 }
