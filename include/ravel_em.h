@@ -5,9 +5,10 @@
  * Every entry point:
  *   - takes raw device pointers of contiguous buffers, sizes and dtype codes
  *     (no framework types cross the ABI);
- *   - enqueues its kernels on `stream` (a hipStream_t), never synchronizes,
- *     never allocates device memory: scratch comes from the caller's
- *     `workspace`, sized by the matching *_workspace() query;
+ *   - enqueues its kernels on `stream` (a hipStream_t), never synchronizes
+ *     (the one exception is the ravel_em_workspace_status() query), never
+ *     allocates device memory: scratch comes from the caller's `workspace`,
+ *     sized by the matching *_workspace() query;
  *   - returns RAVEL_EM_OK (0) or an error code, with a message available from
  *     ravel_em_last_error() (thread-local).  No C++ exception crosses the ABI.
  *
@@ -106,6 +107,30 @@ typedef struct ravel_em_addr_gen {
  */
 int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64_t A,
                        int out_dtype, void* out, void* stream);
+
+/*
+ * Status word of a call.  Every entry point that takes a workspace and sorts
+ * (sort_order, latest_k_fwd, latest_k_resolve, latest1_linear_fwd,
+ * seg_sum_fwd, seg_sum_bwd, cache_prefill) reserves the first
+ * RAVEL_EM_STATUS_BYTES of its workspace for a header whose uint32 at offset 0
+ * is the call's status word.  The call clears it on `stream` before any other
+ * of its kernels runs, and a bounded device-side wait (the look-back of a sort
+ * pass or of the segmented sum) that runs out of spins ORs its bit in.  The
+ * word is final once the call's work on the stream has completed: 0 means
+ * every wait completed; any bit set means the call's outputs are not valid,
+ * although the call itself returned RAVEL_EM_OK.  It has no counterpart in the
+ * reference, whose library sort and scan cannot give up.
+ * ravel_em_workspace_status() copies the word to *status and synchronizes
+ * `stream` (not for use inside graph capture); callers that must not
+ * synchronize can copy the word themselves, stream-ordered.
+ */
+#define RAVEL_EM_STATUS_BYTES 256
+enum {
+  RAVEL_EM_STATUS_SORT_WAIT = 1, /* a sort pass's tile look-back gave up */
+  RAVEL_EM_STATUS_SUM_WAIT = 2   /* the segmented sum's part look-back gave up */
+};
+int ravel_em_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
+                              void* stream);
 
 /* Message of the last failed call on this thread ("" when none). */
 const char* ravel_em_last_error(void);

@@ -145,6 +145,30 @@ def seg_sum(write, payload, read=None, *, address_space: int, write_mask=None):
     return torch.from_numpy(out), torch.from_numpy(mask.astype(bool))
 
 
+def seg_sum_grad(write, grad_out, read=None, *, address_space: int, write_mask=None):
+    """Gradient of causal_sum_lookup's sums with respect to the payload, fp64:
+    (grad [B,T,C,D], S [B,T,C,D] the sum of |grad_out| terms, n [B,T,C,1] the
+    number of terms).  A write at time t collects grad_out of the reads of its
+    stream strictly after t (ravel_lm/ravel_memory.py:216-241 is linear in the
+    payload); that is the forward sum on the time-reversed tape with the roles
+    of reads and writes swapped, zero for masked writes.  Pinned by autograd
+    of the dense per-stream matrix form (tests/test_oracle.py)."""
+    rd = write if read is None else read
+    w, r = _np_i64(write), _np_i64(rd)
+    wf = torch.from_numpy(np.ascontiguousarray(w[:, ::-1]))
+    rf = torch.from_numpy(np.ascontiguousarray(r[:, ::-1]))
+    gf = grad_out.detach().cpu().flip(1)
+    g, _ = seg_sum(rf, gf, wf, address_space=address_space)
+    s, _ = seg_sum(rf, gf.abs(), wf, address_space=address_space)
+    ones = torch.ones(*w.shape, 1, dtype=torch.float64)
+    n, _ = seg_sum(rf, ones, wf, address_space=address_space)
+    g, s, n = g.flip(1), s.flip(1), n.flip(1)
+    if write_mask is not None:
+        keep = torch.as_tensor(_np_mask(write_mask).astype(bool)).view(*w.shape[:2], 1, 1).double()
+        g, s, n = g * keep, s * keep, n * keep
+    return g, s, n
+
+
 def cache_prefill(write, payload, *, address_space: int, k: int, write_mask=None):
     """Oracle of T sequential cache writes: (values [B,C,A,k,D], filled [B,C,A,k])."""
     w = _np_i64(write)

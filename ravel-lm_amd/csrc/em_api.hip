@@ -173,9 +173,20 @@ int check_ws(const Bump& plan, size_t have) {
   return RAVEL_EM_OK;
 }
 
-// Workspace of one sort.
+// A call with no records launches no sort; it still leaves a clear status
+// word behind when it was given a workspace that holds one.
+int clear_status(void* ws, size_t wsb, void* stream) {
+  if (!ws || wsb < sizeof(uint32_t)) return RAVEL_EM_OK;
+  const hipError_t e = fill_bytes(ws, 0, sizeof(uint32_t), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "status word");
+  return RAVEL_EM_OK;
+}
+
+// Workspace of one sort.  Every workspace that holds a sort starts with the
+// call's status header (the status word at offset 0).
 template <typename U>
 struct SortWs {
+  uint32_t* status;
   U* ka;
   U* kb;
   uint32_t* counts;
@@ -184,6 +195,7 @@ struct SortWs {
 template <typename U>
 SortWs<U> take_sort(Bump& bp, const Tape& tp) {
   SortWs<U> w;
+  w.status = bp.take<uint32_t>(kStatusBytes / sizeof(uint32_t));
   w.ka = bp.take<U>((size_t)tp.n());
   w.kb = bp.take<U>((size_t)tp.n());
   w.counts = bp.take<uint32_t>(sort_counts_words(tp));
@@ -234,12 +246,14 @@ struct LkPlan {
 
 template <typename U>
 int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
-                 const void* payload, int64_t row_bytes, const Tape& tp, int64_t k,
+                 const void* payload, int64_t row_bytes, const Tape& tape, int64_t k,
                  void* out_values, uint8_t* out_mask, int32_t* out_src, void* ws, size_t wsb,
                  hipStream_t s) {
   const bool link = !ra && !wmask;
   Bump bp(ws);
+  Tape tp = tape;
   SortWs<U> sw = take_sort<U>(bp, tp);
+  tp.status = sw.status;
   // The link writes segment-major sources (src_seg), which one tiled
   // transpose turns record-major; the read search writes them record-major.
   int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
@@ -286,10 +300,12 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
 
 template <typename U>
 int resolve_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
-                const Tape& tp, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
+                const Tape& tape, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
   const bool link = !ra && !wmask;
   Bump bp(ws);
+  Tape tp = tape;
   SortWs<U> sw = take_sort<U>(bp, tp);
+  tp.status = sw.status;
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;
   if (link && link_short_applies(tp, k)) {  // short tapes: sort and link per segment in LDS
@@ -353,7 +369,7 @@ SumWs<U> take_sum(Bump& bp, const Tape& tp, int64_t D, int dtype, bool direct, b
   if (!direct) {
     w.spos = bp.take<int32_t>((size_t)tp.n());
     if (backward)
-      w.gacc = bp.take<char>((size_t)tp.n() * (size_t)D * (dtype == kF64 ? 8 : 4));
+      w.gacc = bp.take<char>((size_t)tp.n() * (size_t)D * ((dtype == kF64 || dtype == kF32) ? 8 : 4));
     else
       w.S = bp.take<char>((size_t)tp.n() * (size_t)D * dtype_size(dtype));
   }
@@ -362,11 +378,13 @@ SumWs<U> take_sum(Bump& bp, const Tape& tp, int64_t D, int dtype, bool direct, b
 
 template <typename U>
 int seg_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
-                const void* payload, int dtype, const Tape& tp, int64_t D, void* out_sum,
+                const void* payload, int dtype, const Tape& tape, int64_t D, void* out_sum,
                 uint8_t* out_mask, void* ws, size_t wsb, hipStream_t s) {
   const bool direct = !ra && !wmask;
   Bump bp(ws);
+  Tape tp = tape;
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, false);
+  tp.status = w.sw.status;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
@@ -394,11 +412,13 @@ int seg_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
 
 template <typename U>
 int seg_sum_bwd_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
-                    const void* grad, int dtype, const Tape& tp, int64_t D, void* grad_payload,
+                    const void* grad, int dtype, const Tape& tape, int64_t D, void* grad_payload,
                     void* ws, size_t wsb, hipStream_t s) {
   const bool direct = !ra && !wmask;
   Bump bp(ws);
+  Tape tp = tape;
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, true);
+  tp.status = w.sw.status;
   if (int rc = check_ws(bp, wsb)) return rc;
   U* sorted = nullptr;
   hipError_t e = sort_call<U>(wa, wmask, tp, w.sw, &sorted, s, (uint32_t*)w.walk,
@@ -472,7 +492,20 @@ extern "C" {
 
 const char* ravel_em_last_error(void) { return g_err.c_str(); }
 
-int ravel_em_abi_version(void) { return 2; }
+int ravel_em_abi_version(void) { return 3; }
+
+int ravel_em_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
+                              void* stream) {
+  g_err.clear();
+  if (!workspace || !status) return fail(RAVEL_EM_EINVAL, "null pointer");
+  if (workspace_bytes < sizeof(uint32_t))
+    return fail(RAVEL_EM_EINVAL, "a workspace of %zu bytes holds no status word", workspace_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipMemcpyAsync(status, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "status word");
+  return RAVEL_EM_OK;
+}
 
 int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64_t A,
                        int out_dtype, void* out, void* stream) {
@@ -553,8 +586,8 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
   g_err.clear();
   if (int rc = check_tape(B, T, C, A)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
-  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return RAVEL_EM_OK;
+  Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !out_sorted_keys || !out_order) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrIn wa;
   if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
@@ -564,6 +597,7 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
     using U = decltype(tag);
     Bump bp(workspace);
     SortWs<U> sw = take_sort<U>(bp, tp);
+    tp.status = sw.status;
     int64_t* vprefix = write_mask ? bp.take<int64_t>((size_t)(B * T + 1)) : nullptr;
     if (int rc = check_ws(bp, workspace_bytes)) return rc;
     U* sorted = nullptr;
@@ -600,7 +634,7 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
   if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
     return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !out_values || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
@@ -635,7 +669,7 @@ int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int
   if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
     return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !out_src) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
@@ -672,7 +706,7 @@ int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, i
                 "the fused latest-1 linear needs P %% 8 == 0, M %% 8 == 0, M <= 256 and 16-byte "
                 "aligned payload, weight and output (P=%lld M=%lld)",
                 (long long)P, (long long)M);
-  if (B * T * C == 0) return RAVEL_EM_OK;
+  if (B * T * C == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !weight || !out) return fail(RAVEL_EM_EINVAL, "null pointer");
   // Sources: into out_src when given, else at the end of the workspace.
   const size_t rws = ravel_em_latest_k_resolve_workspace(B, T, C, A, 1, read_addr != nullptr, 0);
@@ -772,7 +806,7 @@ int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !out_sum || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
@@ -804,7 +838,7 @@ int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return RAVEL_EM_OK;
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !grad_sum || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
@@ -897,19 +931,22 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
   AddrIn wa;
   if (B * T * C > 0)
     if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
-  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
+  Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
   hipStream_t s = (hipStream_t)stream;
   const int64_t row_bytes = D * dtype_size(payload_dtype);
   auto run = [&](auto tag) -> int {
     using U = decltype(tag);
     Bump bp(workspace);
     SortWs<U> sw = take_sort<U>(bp, tp);
+    tp.status = sw.status;
     if (int rc = check_ws(bp, workspace_bytes)) return rc;
     U* sorted = nullptr;
     hipError_t e = hipSuccess;
     if (tp.n() > 0) {
       e = sort_call<U>(wa, write_mask, tp, sw, &sorted, s);
       if (e != hipSuccess) return hip_fail(e, "sort");
+    } else if (int rc = clear_status(workspace, workspace_bytes, stream)) {
+      return rc;
     }
     e = cache_prefill<U>(sorted, payload, tp, k, row_bytes, values, filled, s);
     if (e != hipSuccess) return hip_fail(e, "cache prefill");

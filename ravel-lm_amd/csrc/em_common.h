@@ -36,6 +36,7 @@ struct Tape {
   bool trunc32 = false; // reference key dtype is int32: addresses pass through int32 first
   int mode = kWrap;
   bool fused = true;    // use the fused sort when its LDS budget holds
+  uint32_t* status = nullptr;  // the call's status word (device), see kStatusSortWait
   int64_t nseg() const { return B * C; }
   int64_t n() const { return B * T * C; }
   bool wide() const { return abits + tbits > 32; }
@@ -70,6 +71,14 @@ struct AddrIn {
   const void* dense = nullptr;
   AddrGen gen;
 };
+
+// Status word of a call: word 0 of the caller's workspace (kStatusBytes are
+// reserved there).  The call's first kernel clears it; a bounded look-back
+// wait that runs out of spins ORs its bit in (the call's results are then
+// wrong).  Values match RAVEL_EM_STATUS_* of the C ABI header.
+constexpr uint32_t kStatusSortWait = 1u;  // a sort pass's tile look-back
+constexpr uint32_t kStatusSumWait = 2u;   // the segmented sum's part look-back
+constexpr size_t kStatusBytes = 256;
 
 int bit_width_u64(uint64_t x);
 Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);

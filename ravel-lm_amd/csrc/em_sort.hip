@@ -32,8 +32,10 @@ constexpr int kPackTT = 64;  // time steps per pack block (upper bound)
 template <typename U, typename AS>
 __global__ __launch_bounds__(256) void pack_keys_kernel(
     const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
-    int64_t A, int tbits, int mode, int trunc32, int tt_max, U* __restrict__ keys) {
+    int64_t A, int tbits, int mode, int trunc32, int tt_max, U* __restrict__ keys,
+    uint32_t* __restrict__ status) {
   extern __shared__ unsigned char smem_raw[];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;  // the call's first sort kernel
   U* tile = reinterpret_cast<U*>(smem_raw);  // [C][tt_max + 1]
   const int64_t ntb = (T + tt_max - 1) / tt_max;
   const int64_t b = blockIdx.x / ntb;
@@ -290,10 +292,12 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     const DenseAddr<AT> addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C,
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int h0, int nh, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
-    uint16_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words) {
+    uint16_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words,
+    uint32_t* __restrict__ status) {
   __shared__ __align__(16) U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
   zero_slice(zero, zero_words);  // every block, padding included
+  if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;  // the call's first sort kernel
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
   if (logical >= nlogical) return;  // padding block of the XCD-rounded grid (uniform)
   const int cg = (int)(logical % ncg);
@@ -412,7 +416,6 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint16_t* __restr
   const int lo = slo * m;
   const int hi = (shi * m) < ntiles ? (shi * m) : ntiles;
   if (threadIdx.x < npass) tickets[(int64_t)threadIdx.x * gridDim.x + seg] = 0;  // [pass][seg]
-  if (seg == 0 && threadIdx.x == 0) tickets[(int64_t)npass * gridDim.x] = 0;   // error word
   for (int p = 0; p < nh; ++p) {
     uint32_t sum = 0;
     for (int t0 = lo; t0 < hi; t0 += U8) {
@@ -557,7 +560,7 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
 // (the high digit of a two-pass key) sets modes[seg] = 1 when no bucket of
 // that digit holds more than bucket_max keys (the segment then scatters by the
 // high digit and links by buckets), else 0 (low digit first, look-back link).
-// Resets the look-back tickets of all npass passes and the error word.
+// Resets the look-back tickets of all npass passes.
 constexpr int kShortMaxTiles = 64;
 
 __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
@@ -596,7 +599,6 @@ __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
     if (d == 0) modes[seg] = s_big ? 0u : 1u;
   }
   if (p == 0 && d < npass) tickets[(int64_t)d * nseg + seg] = 0;  // [pass][seg]
-  if (blockIdx.x == 0 && d == 0) tickets[(int64_t)npass * nseg] = 0;  // error word
 }
 
 template <typename U, int ITEMS>
@@ -707,7 +709,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
       if ((w & ~kValMask) == kFlagP) done = true;
     }
   }
-  if (!ok) atomicOr(err, 1u);
+  if (!ok) atomicOr(err, kStatusSortWait);
   if (tile > 0)
     __hip_atomic_store(&st[(int64_t)tile * kRadix + tid], kFlagP | ((excl + own) & kValMask),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -806,7 +808,7 @@ __device__ __forceinline__ void sweep_link_tile(
         if ((x >> 62) == 2) done = true;
       }
     }
-    if (!ok) atomicOr(err, 1u);
+    if (!ok) atomicOr(err, kStatusSortWait);
     if (tile > 0) {
       const bool has = own || found;
       const uint64_t inc = (has ? kLHasKey : 0ull) | (uint64_t)(own ? own_last : lastk) |
@@ -1147,9 +1149,9 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   uint32_t* offs = words + (hist_words + 1) / 2;
   uint32_t* binbase = offs + offs_words;
   uint32_t* status[2] = {binbase + bin_words, binbase + bin_words + status_words};
-  uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then the error word
-  uint32_t* err = tickets + (int64_t)npass * tp.nseg();
-  uint32_t* modes = bucket ? err + tp.nseg() : nullptr;  // after the ticket rows and error row
+  uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then a spare row
+  uint32_t* err = tp.status;  // bounded waits that give up set kStatusSortWait here
+  uint32_t* modes = bucket ? tickets + (int64_t)(npass + 1) * tp.nseg() : nullptr;
   const int64_t nlogical = tp.B * nt0 * ncg;
   const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
   // Divisors of the pack index math (the last head group / time tile of a row
@@ -1165,11 +1167,12 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
       pack_hist_kernel<U, AT, VEC><<<pgrid, kPackThreads, 0, s>>>(
           src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
           nh, nt0, nlogical, make_fastdiv((uint32_t)(pl.CC / VEC)), by_tt, ka, hist, zero,
-          zero_words);
+          zero_words, tp.status);
     } else {
       pack_hist_kernel<U, AT, 1><<<pgrid, kPackThreads, 0, s>>>(
           src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
-          nh, nt0, nlogical, make_fastdiv((uint32_t)pl.CC), by_tt, ka, hist, zero, zero_words);
+          nh, nt0, nlogical, make_fastdiv((uint32_t)pl.CC), by_tt, ka, hist, zero, zero_words,
+          tp.status);
     }
     return hipGetLastError();
   });
@@ -1249,6 +1252,7 @@ template <typename U>
 hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, U* ka,
                      U* kb, uint32_t* counts, U** sorted, hipStream_t s, uint32_t* zero,
                      int64_t zero_words, int32_t* link_seg) {
+  if (!tp.status) return hipErrorInvalidValue;  // every sort clears and may set the call's word
   if (sizeof(U) == 4 && tp.fused && sort_short_applies(tp)) {
     // short tapes: each segment sorted in LDS by one block (the caller links)
     if (zero && zero_words > 0) {
@@ -1275,7 +1279,7 @@ hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, U
   const unsigned grid = (unsigned)(tp.B * ntb);
   hipError_t e = with_addr(addr, tp, [&](auto src) {
     pack_keys_kernel<U, decltype(src)><<<grid, 256, shm, s>>>(
-        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, ka);
+        src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, ka, tp.status);
     return hipGetLastError();
   });
   if (e != hipSuccess) return e;
@@ -1342,7 +1346,7 @@ template <typename AS, int ITEMS, bool LINK, int NT>
 __global__ __launch_bounds__(NT) void seg_sort_link_kernel(
     const AS addr, const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int tbits,
     int npass, int mode, int trunc32, int k, int64_t nseg, int32_t* __restrict__ src,
-    uint32_t* __restrict__ keys_out) {
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ status) {
   constexpr int NW = NT / kWave;
   __shared__ uint32_t wcnt[NW][kRadix];
   __shared__ uint32_t dstart[kRadix];
@@ -1350,6 +1354,7 @@ __global__ __launch_bounds__(NT) void seg_sort_link_kernel(
   __shared__ uint32_t buf[2][kShortT];
   __shared__ uint16_t inv[kShortT];
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+  if (blockIdx.x == 0 && tid == 0) *status = 0;  // the call's first sort kernel
   const int64_t seg = xcd_block(blockIdx.x, gridDim.x);
   if (seg >= nseg) return;  // uniform per block
   const int64_t b = seg / C, c = seg - (seg / C) * C;
@@ -1455,7 +1460,7 @@ hipError_t seg_sort_short(const AddrIn& addr, const uint8_t* wmask, const Tape& 
 #define REM_SL(IT)                                                                            \
   seg_sort_link_kernel<decltype(a), IT, LINK, kShortThreads><<<grid, kShortThreads, 0, s>>>(   \
       a, wmask, tp.T, tp.C, tp.A, tp.tbits, npass, tp.mode, tp.trunc32 ? 1 : 0, k, tp.nseg(), \
-      src, keys_out)
+      src, keys_out, tp.status)
     if (tp.T <= kShortThreads)
       REM_SL(1);
     else if (tp.T <= 2 * kShortThreads)
@@ -1477,7 +1482,7 @@ bool link_short_applies(const Tape& tp, int64_t k) {
 
 hipError_t link_short(const AddrIn& addr, const Tape& tp, int k, int32_t* src, hipStream_t s) {
   if (tp.n() == 0) return hipSuccess;
-  if (!link_short_applies(tp, k)) return hipErrorInvalidValue;
+  if (!link_short_applies(tp, k) || !tp.status) return hipErrorInvalidValue;
   return seg_sort_short<true>(addr, nullptr, tp, k, src, nullptr, s);
 }
 

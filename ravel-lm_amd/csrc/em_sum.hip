@@ -332,7 +332,7 @@ template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF,
 __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int G, int64_t nparts, XOut* __restrict__ out, uint8_t* __restrict__ omask,
-    uint64_t* __restrict__ status, uint64_t* __restrict__ tickets) {
+    uint64_t* __restrict__ status, uint64_t* __restrict__ tickets, uint32_t* __restrict__ err) {
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
   using OutV = typename Unit<CPU * (int)sizeof(XOut)>::T;
   constexpr int NWMAX = kWalkThreads;  // walkers when G == 1
@@ -422,34 +422,47 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 #pragma unroll
   for (int j = 0; j < CPU; ++j) tl[w * (G * CPU) + v * CPU + j] = acc[j];
   __syncthreads();
-  // 3. part aggregate, look-back over earlier parts, carry-in of every walker
+  // 3. part aggregate, look-back over earlier parts, carry-in of every walker.
+  // One thread per accumulator column; rows of 16-bit values have up to
+  // 64 * 8 = 512 columns, so a thread may own two.  Every column of a part is
+  // published before any column waits on an earlier part.
   const int ncol = G * CPU;  // == D
   constexpr int PW = Pub<Acc>::W;
-  if (tid < ncol) {
-    Acc run = Acc(0);
-    bool any = false;
-    for (int k = 0; k < NW; ++k) {
-      const Acc t = tl[k * ncol + tid];
-      run = hs[k] ? t : run + t;
-      any = any || hs[k];
-    }
-    uint64_t* sp = status + ((seg * nparts + q) * ncol + tid) * PW;
-    Pub<Acc>::put(sp, run, any ? 2u : 1u);
-    Acc carry = Acc(0);
-    for (int64_t j = q - 1; j >= 0; --j) {
-      Acc val;
-      uint32_t f;
-      if (!Pub<Acc>::get(status + ((seg * nparts + j) * ncol + tid) * PW, &val, &f)) {
-        atomicOr((unsigned long long*)&tickets[gridDim.x / nparts], 1ull);  // error word
-        break;
+  constexpr int kColsPerThread = (64 * CPU + kWalkThreads - 1) / kWalkThreads;
+  bool any = false;
+  for (int k = 0; k < NW; ++k) any = any || hs[k];
+#pragma unroll
+  for (int cc = 0; cc < kColsPerThread; ++cc) {
+    const int col = tid + cc * kWalkThreads;
+    if (col < ncol) {
+      Acc run = Acc(0);
+      for (int k = 0; k < NW; ++k) {
+        const Acc t = tl[k * ncol + col];
+        run = hs[k] ? t : run + t;
       }
-      carry = val + carry;
-      if (f == 2u) break;
+      Pub<Acc>::put(status + ((seg * nparts + q) * ncol + col) * PW, run, any ? 2u : 1u);
     }
-    for (int k = 0; k < NW; ++k) {
-      const Acc t = tl[k * ncol + tid];
-      tl[k * ncol + tid] = carry;
-      carry = hs[k] ? t : carry + t;
+  }
+#pragma unroll
+  for (int cc = 0; cc < kColsPerThread; ++cc) {
+    const int col = tid + cc * kWalkThreads;
+    if (col < ncol) {
+      Acc carry = Acc(0);
+      for (int64_t j = q - 1; j >= 0; --j) {
+        Acc val;
+        uint32_t f;
+        if (!Pub<Acc>::get(status + ((seg * nparts + j) * ncol + col) * PW, &val, &f)) {
+          atomicOr(err, kStatusSumWait);
+          break;
+        }
+        carry = val + carry;
+        if (f == 2u) break;
+      }
+      for (int k = 0; k < NW; ++k) {
+        const Acc t = tl[k * ncol + col];
+        tl[k * ncol + col] = carry;
+        carry = hs[k] ? t : carry + t;
+      }
     }
   }
   __syncthreads();
@@ -494,6 +507,7 @@ hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D,
   const int64_t in_bytes = D * (int64_t)sizeof(XIn);
   const int64_t G = in_bytes / 16;
   const int out_unit = 16 / (int)sizeof(XIn) * (int)sizeof(XOut);
+  if (!tp.status) return hipErrorInvalidValue;  // the walker's waits report into the call's word
   if (walk && in_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
       ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & (uintptr_t)(out_unit - 1)) == 0 &&
       tp.T < ((int64_t)1 << 31)) {
@@ -503,7 +517,7 @@ hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D,
     uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
     segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK>
         <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, (int)G,
-                                                   nparts, out, omask, walk, tickets);
+                                                   nparts, out, omask, walk, tickets, tp.status);
     return hipGetLastError();
   }
   const int64_t nch_seg = (tp.T + kChunk - 1) / kChunk;
@@ -562,7 +576,9 @@ hipError_t seg_sum_bwd_t(const U* sorted, const int32_t* spos, const void* grad_
     return run_segsum<U, S, S, Acc, E, E, true, false, false, false, false>(
         sorted, (const S*)grad_out, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag,
         (Acc*)carry, walk, s);
-  using G = typename std::conditional<DT == kF64, double, float>::type;
+  // read gradients gathered per sorted write position: fp64 for 32/64-bit
+  // payloads (their sums accumulate in fp64 throughout), fp32 for 16-bit ones
+  using G = typename std::conditional<DT == kF64 || DT == kF32, double, float>::type;
   const int64_t N = tp.n();
   hipError_t e = fill_bytes(gacc, 0, (size_t)(N * D) * sizeof(G), s);
   if (e != hipSuccess) return e;
@@ -583,8 +599,8 @@ size_t seg_sum_chunks(const Tape& tp) {
 size_t acc_bytes(int dtype) { return (dtype == kF32 || dtype == kF64) ? 8 : 4; }
 
 size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype) {
-  // part aggregates, then one ticket per segment and the error word
-  return seg_sum_status_words(tp, D, acc_bytes(dtype)) + (size_t)tp.nseg() + 1;
+  // part aggregates, then one ticket per segment
+  return seg_sum_status_words(tp, D, acc_bytes(dtype)) + (size_t)tp.nseg();
 }
 
 template <typename U>

@@ -48,6 +48,7 @@ class AddrGen(ctypes.Structure):
 # name -> (restype, argtypes); must list every function of include/ravel_em.h
 SIGNATURES = {
     "ravel_em_last_error": (ctypes.c_char_p, []),
+    "ravel_em_workspace_status": (_i, [_vp, _sz, _vp, _vp]),
     "ravel_em_abi_version": (_i, []),
     "ravel_em_addresses": (_i, [_vp, _i64, _i64, _i64, _i, _vp, _vp]),
     "ravel_em_key_bits": (_i, [_i64, _i64, _i64, _i64]),
@@ -202,3 +203,55 @@ def require_device(*tensors: Optional[torch.Tensor]) -> None:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# Status words (include/ravel_em.h): bit values of the word at offset 0 of a
+# sorting call's workspace.
+STATUS_SORT_WAIT, STATUS_SUM_WAIT = 1, 2
+_STATUS_NAMES = {STATUS_SORT_WAIT: "a sort look-back wait gave up",
+                 STATUS_SUM_WAIT: "a segmented-sum look-back wait gave up"}
+
+
+class DeviceWaitError(NativeLibraryError):
+    """A call returned OK but one of its bounded device waits gave up, so its
+    outputs are not valid (the call's status word is non-zero)."""
+
+
+# Opt-in: after every sorting call, read the status word back (this
+# synchronizes the stream, so it is meant for tests and debugging) and raise
+# DeviceWaitError when it is non-zero.  Calls made while a HIP graph is being
+# captured are not checked.  RAVEL_EM_CHECK_STATUS=1 turns it on at import.
+_status_check = os.environ.get("RAVEL_EM_CHECK_STATUS", "") == "1"
+status_checks = 0  # number of status words read so far
+
+
+def set_status_check(on: bool) -> bool:
+    """Turn the status read-back on or off; returns the previous setting."""
+    global _status_check
+    prev, _status_check = _status_check, bool(on)
+    return prev
+
+
+def status_word(ws: torch.Tensor) -> int:
+    """The status word of the last call that used workspace ws (synchronizes
+    the current stream of ws's device)."""
+    word = ctypes.c_uint32(0)
+    check(library().ravel_em_workspace_status(ws.data_ptr(), ws.numel(), ctypes.byref(word),
+                                              stream_of(ws)))
+    return int(word.value)
+
+
+def raise_for_status(word: int) -> None:
+    if word:
+        names = [n for b, n in _STATUS_NAMES.items() if word & b] or ["unknown bits"]
+        raise DeviceWaitError(f"ravel_em status word {word:#x}: {'; '.join(names)}; "
+                              "the call's outputs are not valid")
+
+
+def after_call(ws: torch.Tensor) -> None:
+    """Check the status word of the call that just used ws, when enabled."""
+    global status_checks
+    if not _status_check or torch.cuda.is_current_stream_capturing():
+        return
+    status_checks += 1
+    raise_for_status(status_word(ws))

@@ -64,6 +64,7 @@ def latest_k_impl(
         nat.ptr(values), nat.ptr(mask), nat.ptr(src) if want_src else None,
         nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
     )
+    nat.after_call(ws)
     return values, mask, src
 
 
@@ -164,6 +165,7 @@ def seg_sum_impl(
         nat.ptr(write_mask), nat.ptr(payloads), code, B, T, C, D, address_space,
         nat.ptr(out), nat.ptr(mask), nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
     )
+    nat.after_call(ws)
     return out, mask
 
 
@@ -208,6 +210,7 @@ def seg_sum_backward(
         nat.ptr(write_mask), nat.ptr(grad_sum), code, B, T, C, D, address_space,
         nat.ptr(grad_payload), nat.ptr(ws), ws.numel(), nat.stream_of(grad_sum),
     )
+    nat.after_call(ws)
     return grad_payload
 
 
@@ -254,6 +257,7 @@ def sort_order(write_addresses: Tensor, write_mask: Optional[Tensor], address_sp
         B, T, C, address_space, nat.ptr(keys), nat.ptr(order), nat.ptr(ws), ws.numel(),
         nat.stream_of(write_addresses),
     )
+    nat.after_call(ws)
     return keys, order
 
 
@@ -313,3 +317,4 @@ def cache_prefill(write_addresses: Tensor, payloads: Tensor, write_mask: Optiona
         nat.ptr(payloads), nat.payload_code(payloads.dtype), B, T, C, D, address_space, k,
         nat.ptr(values), nat.ptr(filled), nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
     )
+    nat.after_call(ws)

@@ -288,6 +288,7 @@ def latest_k_gen(tokens: Optional[Tensor], history: Optional[Tensor],
         nat.payload_code(payloads.dtype), B, T, C, D, address_space, k, nat.ptr(values),
         nat.ptr(mask), nat.ptr(src) if want_src else None, nat.ptr(ws), ws.numel(),
         nat.stream_of(payloads)))
+    nat.after_call(ws)
     return values, mask, src
 
 
@@ -341,6 +342,7 @@ def seg_sum_gen(tokens: Optional[Tensor], history: Optional[Tensor],
         nat.ref(w), nat.ref(r), nat.ADDR_GEN, nat.ptr(write_mask), nat.ptr(payloads), code,
         B, T, C, D, address_space, nat.ptr(out), nat.ptr(mask), nat.ptr(ws), ws.numel(),
         nat.stream_of(payloads)))
+    nat.after_call(ws)
     return out, mask
 
 
@@ -371,6 +373,7 @@ def seg_sum_gen_backward(tokens: Optional[Tensor], history: Optional[Tensor],
         nat.ref(w), nat.ref(r), nat.ADDR_GEN, nat.ptr(write_mask), nat.ptr(grad_sum), code,
         B, T, C, D, address_space, nat.ptr(grad_payload), nat.ptr(ws), ws.numel(),
         nat.stream_of(grad_sum)))
+    nat.after_call(ws)
     return grad_payload
 
 

@@ -53,6 +53,7 @@ def _latest1_linear(write_addresses: Tensor, payloads: Tensor, read_addresses: O
             nat.ptr(payloads), nat.payload_code(payloads.dtype), nat.ptr(weight),
             B, T, C, P, M, address_space, nat.ptr(out), nat.ptr(src), nat.ptr(ws), ws.numel(),
             nat.stream_of(payloads)))
+        nat.after_call(ws)
         return out, src
     values, _, s = _ops.latest_k(write_addresses, payloads, read_addresses, None, address_space, 1, True)
     out = torch.matmul(values.reshape(B * T, C * P), weight.t()).reshape(B, T, M)
@@ -121,6 +122,7 @@ def _latest1_linear_gen(tokens: Optional[Tensor], history: Optional[Tensor],
             nat.ref(w), nat.ref(r), nat.ADDR_GEN, nat.ptr(payloads), nat.payload_code(payloads.dtype),
             nat.ptr(weight), B, T, C, P, M, address_space, nat.ptr(out), nat.ptr(src), nat.ptr(ws),
             ws.numel(), nat.stream_of(payloads)))
+        nat.after_call(ws)
         return out, src
     from .addressing import latest_k_gen
 

@@ -19,6 +19,23 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
 
 
+@pytest.fixture(autouse=True)
+def _check_status_words(request):
+    """GPU tests read back the status word of every sorting call (see
+    ravel_em._native.after_call): a bounded device wait that gave up fails the
+    test with DeviceWaitError instead of passing with wrong outputs."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    from ravel_em import _native as nat
+
+    prev = nat.set_status_check(True)
+    try:
+        yield
+    finally:
+        nat.set_status_check(prev)
+
+
 @pytest.fixture(scope="session")
 def device():
     import torch

@@ -37,7 +37,60 @@ def test_binding_table_matches_header():
 
 
 def test_abi_version():
-    assert nat.library().ravel_em_abi_version() == 2
+    assert nat.library().ravel_em_abi_version() == 3
+
+
+def test_status_query_rejects_bad_arguments_without_a_device():
+    lib = nat.library()
+    word = ctypes.c_uint32(7)
+    assert lib.ravel_em_workspace_status(None, 256, ctypes.byref(word), None) == 1
+    assert "null" in _err()
+    assert lib.ravel_em_workspace_status(ctypes.c_void_p(0x1000), 3, ctypes.byref(word), None) == 1
+    assert "status word" in _err()
+    assert lib.ravel_em_workspace_status(ctypes.c_void_p(0x1000), 256, None, None) == 1
+
+
+def test_sorting_workspaces_hold_the_status_header():
+    lib = nat.library()
+    hdr = 256  # RAVEL_EM_STATUS_BYTES
+    text = open(HEADER).read()
+    assert re.search(r"#define RAVEL_EM_STATUS_BYTES 256\b", text)
+    assert "RAVEL_EM_STATUS_SORT_WAIT = 1" in text and "RAVEL_EM_STATUS_SUM_WAIT = 2" in text
+    assert (nat.STATUS_SORT_WAIT, nat.STATUS_SUM_WAIT) == (1, 2)
+    # the smallest tapes still reserve the header
+    assert lib.ravel_em_sort_order_workspace(1, 1, 1, 1, 0) >= hdr
+    assert lib.ravel_em_latest_k_workspace(1, 1, 1, 1, 1, 0, 0, 1) >= hdr
+    assert lib.ravel_em_latest_k_resolve_workspace(1, 1, 1, 1, 1, 0, 0) >= hdr
+    assert lib.ravel_em_seg_sum_workspace(1, 1, 1, 8, 1, 0, 0, nat.FLOAT32) >= hdr
+    assert lib.ravel_em_seg_sum_bwd_workspace(1, 1, 1, 8, 1, 0, 0, nat.FLOAT32) >= hdr
+    assert lib.ravel_em_cache_prefill_workspace(1, 0, 1, 1, 0) >= hdr
+    assert lib.ravel_em_latest1_linear_workspace(1, 1, 1, 1, 0, 1) >= hdr
+
+
+def test_status_words_raise_on_the_host(monkeypatch):
+    """The read-back plumbing: a non-zero word raises DeviceWaitError naming
+    the wait; zero passes; nothing is read while checking is off."""
+    nat.raise_for_status(0)
+    with pytest.raises(nat.DeviceWaitError, match="sort look-back"):
+        nat.raise_for_status(nat.STATUS_SORT_WAIT)
+    with pytest.raises(nat.DeviceWaitError, match="segmented-sum look-back"):
+        nat.raise_for_status(nat.STATUS_SUM_WAIT)
+    with pytest.raises(nat.DeviceWaitError, match="0x3"):
+        nat.raise_for_status(3)
+    words = iter([0, nat.STATUS_SUM_WAIT])
+    monkeypatch.setattr(nat, "status_word", lambda ws: next(words))
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    prev = nat.set_status_check(False)
+    try:
+        nat.after_call(None)  # off: no read
+        nat.set_status_check(True)
+        before = nat.status_checks
+        nat.after_call(None)  # reads 0
+        with pytest.raises(nat.DeviceWaitError):
+            nat.after_call(None)  # reads the sum bit
+        assert nat.status_checks == before + 2
+    finally:
+        nat.set_status_check(prev)
 
 
 @pytest.mark.parametrize("shape", [(1, 2048, 3, 1024), (1024, 65536, 64, 65536), (8, 256, 4, 512),

@@ -116,3 +116,46 @@ def test_cfg5_prefill_and_steps_reduced_batch(device):
     vals, filled = oracle.cache_prefill(w_all, p_all, address_space=d.address_space, k=d.k)
     assert torch.equal(cache.filled.cpu(), filled)
     assert torch.equal(cache.values.cpu(), vals)
+
+
+def test_cfg5_full_size(device):
+    """cfg5 at its stated size: a [256, 8, 4096, 4, 64] bf16 cache (2^32 bytes,
+    where 32-bit offset arithmetic would wrap) prefilled from T = 2048, then all
+    1024 fused read-then-write steps.  The final cache against the oracle's
+    sequential replay of all 2048 + 1024 writes; the reads of the first, middle
+    and last steps against the oracle's latest-k sources over the prefix the
+    read sees (the writes before it; a step's own write comes after its read)."""
+    d = workloads.cfg5(device)
+    B, T, C, D = d.prefill_payload.shape
+    S = d.step_read.shape[0]
+    A, k = d.address_space, d.k
+    print(f"[cfg5 full] B={B} T={T} C={C} A={A} k={k} D={D} steps={S}", flush=True)
+    cache = RavelLayerCache.prefill(d.prefill_write, d.prefill_payload, address_space=A, k=k)
+    assert cache.values.numel() * cache.values.element_size() == 1 << 32
+    checked = {0: None, S // 2: None, S - 1: None}
+    for s in range(S):
+        vals, mask = cache.step(d.step_read[s], d.step_write[s], d.step_payload[s])
+        if s in checked:
+            checked[s] = (vals.cpu(), mask.cpu())
+    torch.cuda.synchronize()
+    w_all = torch.cat([d.prefill_write, d.step_write.permute(1, 0, 2)], dim=1).cpu()
+    p_all = torch.cat([d.prefill_payload, d.step_payload.permute(1, 0, 2, 3)], dim=1).cpu()
+    rows = p_all.reshape(-1, D)
+    for s, (vals, mask) in checked.items():
+        tp = T + s + 1  # the read sits at time T + s, after the writes before it
+        r = w_all[:, :tp].clone()
+        r[:, T + s] = d.step_read[s].cpu()
+        src = oracle.latest_k_src(w_all[:, :tp], r, address_space=A, k=k)[:, T + s]  # [B, C, k]
+        s64 = torch.from_numpy(src.astype("int64"))
+        # src indexes the [B, tp, C] prefix tape; map it to rows of p_all
+        b_i, rem = s64 // (tp * C), s64 % (tp * C)
+        flat = (b_i * (T + S) * C + rem).clamp_min(0)
+        want = rows.index_select(0, flat.view(-1)).view(B, C, k, D)
+        want = torch.where((s64 >= 0).unsqueeze(-1), want, torch.zeros((), dtype=want.dtype))
+        assert torch.equal(mask, s64 >= 0), f"step {s} mask"
+        assert torch.equal(vals, want), f"step {s} values"
+        print(f"[cfg5 full] step {s} reads match", flush=True)
+    ov, of = oracle.cache_prefill(w_all, p_all, address_space=A, k=k)
+    assert torch.equal(cache.filled.cpu(), of)
+    assert torch.equal(cache.values.cpu(), ov)
+    print("[cfg5 full] final cache matches the replay", flush=True)

@@ -195,6 +195,27 @@ def test_seg_sum_three_way(seed, B, T, C, A, lo, hi, masked, sep, k):
     torch.testing.assert_close(tv, out, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("seed,B,T,C,A,lo,hi,masked,sep,k", CASES)
+def test_seg_sum_grad_matches_autograd(seed, B, T, C, A, lo, hi, masked, sep, k):
+    """oracle.seg_sum_grad against autograd of the torch restatement of the
+    reference's sum (an independent, differentiable formulation); n against
+    the same autograd with unit gradients."""
+    w, r, m = _rand_case(seed, B, T, C, A, lo, hi, masked, sep)
+    gen = torch.Generator().manual_seed(seed + 300)
+    p = torch.randn(B, T, C, 3, generator=gen, dtype=torch.float64).requires_grad_(True)
+    gy = torch.randn(B, T, C, 3, generator=gen, dtype=torch.float64)
+    tv, _ = torch_ref.seg_sum(w, p, r, address_space=A, write_mask=m)
+    (want,) = torch.autograd.grad(tv, p, gy)
+    g, s, n = oracle.seg_sum_grad(w, gy, r, address_space=A, write_mask=m)
+    torch.testing.assert_close(g, want, rtol=1e-12, atol=1e-12)
+    (want_s,) = torch.autograd.grad(torch_ref.seg_sum(w, p, r, address_space=A, write_mask=m)[0],
+                                    p, gy.abs())
+    torch.testing.assert_close(s, want_s, rtol=1e-12, atol=1e-12)
+    (want_n,) = torch.autograd.grad(torch_ref.seg_sum(w, p, r, address_space=A, write_mask=m)[0],
+                                    p, torch.ones_like(gy))
+    assert torch.equal(n.expand_as(want_n), want_n)
+
+
 def test_cache_prefill_matches_replay():
     g = torch.Generator().manual_seed(11)
     B, T, C, A, k, D = 2, 30, 3, 6, 3, 2
