@@ -196,6 +196,27 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
                           size_t workspace_bytes, void* stream);
 
 /*
+ * ravel_em_latest_k_fwd without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It has no counterpart in the reference.  Arguments
+ * and results are those of ravel_em_latest_k_fwd; the scratch is a static
+ * device array of RAVEL_EM_STATIC_SCRATCH_BYTES that each GPU holds from the
+ * library's load until the process ends.  Lookups whose
+ * ravel_em_latest_k_workspace() exceeds it fail with RAVEL_EM_EINVAL before
+ * any launch (it holds the cfg4 headline: B=4 T=65536 C=16 k=1).  No call
+ * allocates or frees memory.  All calls on one GPU share its array, so calls
+ * that overlap on one GPU (concurrent streams or threads) race and must be
+ * serialized by the caller.  out_status (device, optional) receives the call's
+ * status word (RAVEL_EM_STATUS_*), stream-ordered, when given.
+ */
+#define RAVEL_EM_STATIC_SCRATCH_BYTES (128u << 20)
+int ravel_em_latest_k_fwd_static(const void* write_addr, const void* read_addr, int addr_dtype,
+                                 const uint8_t* write_mask, const void* payload,
+                                 int payload_dtype, int64_t B, int64_t T, int64_t C, int64_t D,
+                                 int64_t A, int64_t k, void* out_values, uint8_t* out_mask,
+                                 int32_t* out_src, uint32_t* out_status, void* stream);
+
+/*
  * The two stages of ravel_em_latest_k_fwd as separate calls, for callers that
  * gather several payload tensors through one resolution or time the stages:
  *   resolve: out_src [B,T,C,k] int32 source record index or -1

@@ -2,8 +2,10 @@
 // include/ravel_em.h).  Host code only: argument checks, workspace planning and
 // the kernel sequence of each operator.
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -441,6 +443,52 @@ size_t sum_ws_t(const Tape& tp, int64_t D, int dtype, bool direct, bool backward
   return bp.off;
 }
 
+// ------------------------------------------- static scratch (no allocation) --
+// ravel_em_latest_k_fwd_static runs out of this array instead of a caller
+// workspace.  Each GPU holds its own copy from the library's load until the
+// process ends.  In host code `scratch` names a host-side stand-in: its device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current, and only that address is ever handed to kernels or copies.
+constexpr size_t kStaticScratchBytes = (size_t)128 << 20;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device of stream s (the current device
+// for the null stream).
+int static_scratch(hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "static scratch: device of the stream");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(RAVEL_EM_EINVAL, "static scratch: device %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = -1;
+      e = hipGetDevice(&cur);
+      if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur >= 0 && cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess || !p) return hip_fail(e, "static scratch: hipGetSymbolAddress");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return RAVEL_EM_OK;
+}
+
+__global__ void copy_word_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst) {
+  if (threadIdx.x == 0) *dst = *src;
+}
+
 }  // namespace
 
 void stage_begin(int stage, hipStream_t s) {
@@ -645,6 +693,33 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
                                   out_mask, out_src, workspace, workspace_bytes, s);
   return latest_k_run<uint32_t>(ap.w, ap.rp, write_mask, payload, row_bytes, tp, k, out_values,
                                 out_mask, out_src, workspace, workspace_bytes, s);
+}
+
+int ravel_em_latest_k_fwd_static(const void* write_addr, const void* read_addr, int addr_dtype,
+                                 const uint8_t* write_mask, const void* payload,
+                                 int payload_dtype, int64_t B, int64_t T, int64_t C, int64_t D,
+                                 int64_t A, int64_t k, void* out_values, uint8_t* out_mask,
+                                 int32_t* out_src, uint32_t* out_status, void* stream) {
+  g_err.clear();
+  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  const size_t need = ravel_em_latest_k_workspace(B, T, C, A, k, read_addr != nullptr,
+                                                  write_mask != nullptr, out_src != nullptr);
+  if (need > kStaticScratchBytes)
+    return fail(RAVEL_EM_EINVAL,
+                "this lookup needs %zu bytes of scratch; the static scratch holds %zu "
+                "(use ravel_em_latest_k_fwd with a workspace)",
+                need, kStaticScratchBytes);
+  void* ws = nullptr;
+  if (int rc = static_scratch((hipStream_t)stream, &ws)) return rc;
+  const int rc = ravel_em_latest_k_fwd(write_addr, read_addr, addr_dtype, write_mask, payload,
+                                       payload_dtype, B, T, C, D, A, k, out_values, out_mask,
+                                       out_src, ws, kStaticScratchBytes, stream);
+  if (rc != RAVEL_EM_OK || !out_status) return rc;
+  copy_word_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const uint32_t*)ws, out_status);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "status word");
+  return RAVEL_EM_OK;
 }
 
 size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,

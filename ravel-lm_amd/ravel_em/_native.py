@@ -62,6 +62,10 @@ SIGNATURES = {
         _i,
         [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "ravel_em_latest_k_fwd_static": (
+        _i,
+        [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp],
+    ),
     "ravel_em_latest_k_resolve_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i]),
     "ravel_em_latest_k_resolve": (
         _i, [_vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _sz, _vp]
