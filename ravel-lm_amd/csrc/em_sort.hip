@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     int64_t A, int tbits, int mode, int trunc32, int TT, int CC, int ncg, int h0, int nh, int ntiles,
     int64_t nlogical, FastDiv by_cc, FastDiv by_tt, U* __restrict__ keys,
     uint16_t* __restrict__ hist, uint32_t* __restrict__ zero, int64_t zero_words,
-    uint32_t* __restrict__ status) {
+    uint32_t* __restrict__ status, int32_t* __restrict__ fill_src) {
   __shared__ __align__(16) U tile[kPackLdsBytes / sizeof(U)];
   __shared__ uint32_t h[kHistWords];
   zero_slice(zero, zero_words);  // every block, padding included
@@ -375,13 +375,17 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
     for (int i = threadIdx.x; i < cc * q; i += kPackThreads) {
       const int cl = i / q;
       const int tq = (i - cl * q) << 2;
-      *(u32x4*)&keys[(b * C + c0 + cl) * T + t0 + tq] = *(const u32x4*)&tile[cl * pitch + tq];
+      const int64_t o = (b * C + c0 + cl) * T + t0 + tq;
+      *(u32x4*)&keys[o] = *(const u32x4*)&tile[cl * pitch + tq];
+      if (fill_src) *(u32x4*)&fill_src[o] = u32x4{~0u, ~0u, ~0u, ~0u};
     }
   } else {
     for (int i = threadIdx.x; i < n; i += kPackThreads) {
       const int cl = (int)fdiv_or((uint32_t)i, by_tt, (uint32_t)tt);
       const int tl = i - cl * tt;
-      keys[(b * C + c0 + cl) * T + t0 + tl] = tile[cl * pitch + tl];
+      const int64_t o = (b * C + c0 + cl) * T + t0 + tl;
+      keys[o] = tile[cl * pitch + tl];
+      if (fill_src) fill_src[o] = -1;
     }
   }
   // hist layout [seg][tile][pass][256] of 16-bit counts: one contiguous run per head.
@@ -900,7 +904,7 @@ __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, in
                                              int64_t end, int tbits, uint64_t* mt, uint32_t* lt,
                                              int32_t vbase, int32_t Ci, int32_t* __restrict__ dst,
                                              uint32_t* u) {
-  const int lane = threadIdx.x % kWave;
+  const int lane = __lane_id();
   const uint32_t tmask = (1u << tbits) - 1u;
   const uint64_t bit = 1ull << lane;
   const uint64_t below_mask = bit - 1ull;
@@ -908,46 +912,53 @@ __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, in
 #pragma unroll
   for (int i = 0; i < kRadix / kWave; ++i) lt[i * kWave + lane] = 0;
   __builtin_amdgcn_wave_barrier();
+  // Only the steps of the run are loaded (a wave-uniform count); lanes past
+  // the end of the last step load the run's last key again, so every index
+  // stays inside the run.  Such a copy sits above the key it repeats, shares
+  // its digit and time, and so changes nobody's predecessor and writes the
+  // same table entry; it only must not store.
+  const int n = __builtin_amdgcn_readfirstlane((int)(end - start));  // 0 .. kLinkRun
+  const int nst = (n + kWave - 1) / kWave;
+  const uint32_t* kr = kk + start;
 #pragma unroll
   for (int st = 0; st < kLinkSteps; ++st) {
-    const int64_t idx = start + st * kWave + lane;
-    u[st] = idx < end ? kk[idx] : 0u;
+    if (st < nst) {
+      const int i = st * kWave + lane;
+      u[st] = kr[i < n ? i : n - 1];
+    }
   }
   uint32_t first = 0;  // steps whose key had no predecessor inside the run
 #pragma unroll
   for (int st = 0; st < kLinkSteps; ++st) {
-    if (start + st * kWave >= end) break;  // uniform
-    const bool valid = start + st * kWave + lane < end;
+    if (st >= nst) break;  // uniform
     const uint32_t d = (u[st] >> tbits) & (kRadix - 1);
     const uint32_t tm = u[st] & tmask;
-    // lane 0 is valid in every step that runs
     const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
-    const bool rest = valid && d != d0;
-    const uint64_t eq0 = __ballot(valid && d == d0);
-    if (rest) atomicOr((unsigned long long*)&mt[d], (unsigned long long)bit);
+    const bool rest = d != d0;
+    uint64_t peers = __ballot(!rest);
+    // A wave's LDS operations execute in issue order (the wave barriers keep
+    // the compiler from moving them), so each read sees the writes of earlier
+    // steps and of this step's earlier instructions.
+    if (rest) {  // one LDS round for the lanes off lane 0's digit
+      atomicOr((unsigned long long*)&mt[d], (unsigned long long)bit);
+      __builtin_amdgcn_wave_barrier();
+      peers = mt[d];
+    }
+    const uint32_t carry = lt[d];
     __builtin_amdgcn_wave_barrier();
-    uint64_t peers = eq0;
-    if (rest) peers = mt[d];
-    const uint32_t carry = valid ? lt[d] : 0u;
-    __builtin_amdgcn_wave_barrier();
-    if (valid && (peers & above_mask) == 0) {  // the digit's highest lane in this step
-      if (rest) mt[d] = 0;
+    if ((peers & above_mask) == 0) {  // the digit's highest lane in this step
+      mt[d] = 0;  // (only lanes off lane 0's digit set it; clearing lane 0's is harmless)
       lt[d] = kLHas32 | tm;
     }
     __builtin_amdgcn_wave_barrier();
     const uint64_t lower = peers & below_mask;
-    const int jl = lower ? 63 - __builtin_clzll(lower) : lane;
-    const uint32_t pt = (uint32_t)__shfl((int)tm, jl, kWave);
-    if (valid) {
-      if (lower)
-        dst[tm] = vbase + (int32_t)pt * Ci;
-      else if (carry)
-        dst[tm] = vbase + (int32_t)(carry & ~kLHas32) * Ci;
-      else if (!COOP)
-        dst[tm] = -1;
-      else
-        first |= 1u << st;
-    }
+    const int jl = 63 - __builtin_clzll(lower | 1ull);  // lane 0 when there is no lower peer
+    const uint32_t pt = (uint32_t)__builtin_amdgcn_ds_bpermute(jl << 2, (int)tm);
+    const bool has = lower != 0 || carry != 0;
+    const uint32_t pred = lower != 0 ? pt : (carry & ~kLHas32);
+    const bool valid = st * kWave + lane < n;
+    if (COOP && valid && !has) first |= 1u << st;
+    if (valid && has) dst[tm] = vbase + (int32_t)pred * Ci;  // -1 entries are pre-filled
   }
   return first;
 }
@@ -1033,7 +1044,7 @@ __global__ __launch_bounds__(kLinkThreads) void bucket_link_kernel(
       for (int st = 0; st < kLinkSteps; ++st) {
         if ((first >> st) & 1u) {
           const uint32_t cy = ctab[w][(u[st] >> tbits) & (kRadix - 1)];
-          dst[u[st] & tmask] = cy ? vbase + (int32_t)(cy & ~kLHas32) * Ci : -1;
+          if (cy) dst[u[st] & tmask] = vbase + (int32_t)(cy & ~kLHas32) * Ci;  // else pre-filled -1
         }
       }
     }
@@ -1167,12 +1178,12 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
       pack_hist_kernel<U, AT, VEC><<<pgrid, kPackThreads, 0, s>>>(
           src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
           nh, nt0, nlogical, make_fastdiv((uint32_t)(pl.CC / VEC)), by_tt, ka, hist, zero,
-          zero_words, tp.status);
+          zero_words, tp.status, bucket ? link_seg : nullptr);
     } else {
       pack_hist_kernel<U, AT, 1><<<pgrid, kPackThreads, 0, s>>>(
           src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
           nh, nt0, nlogical, make_fastdiv((uint32_t)pl.CC), by_tt, ka, hist, zero, zero_words,
-          tp.status);
+          tp.status, bucket ? link_seg : nullptr);
     }
     return hipGetLastError();
   });
