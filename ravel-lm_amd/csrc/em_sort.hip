@@ -642,6 +642,107 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
 }
 
+// Sums over pack tiles of one histogram pass of a segment, for the pass-0
+// scatter of bucket mode without an offsets kernel: thread d gets bef = count
+// of digit d in the pack tiles before `lo` and tot = its count in all nt0
+// tiles.  Thread (g, u) loads 16-byte units (digits 8u..8u+7) of the tiles
+// i = g (mod 8); the eight groups' partial sums meet in `part` (LDS, 16-bit:
+// at most 8 tiles of at most 2048 keys each).
+template <int NT>
+__device__ __forceinline__ void hist_sums(const uint16_t* __restrict__ hs, int per, int nt0,
+                                          int lo, uint16_t* part, uint32_t* bef, uint32_t* tot) {
+  static_assert(NT == 256, "one thread per digit");
+  constexpr int kG = NT / 32;  // tile groups
+  const int tid = threadIdx.x, g = tid >> 5, u = tid & 31;
+  u32x4 v[kShortMaxTiles / kG];
+#pragma unroll
+  for (int r = 0; r < kShortMaxTiles / kG; ++r) {
+    const int i = r * kG + g;
+    v[r] = i < nt0 ? *(const u32x4*)(hs + (int64_t)i * per + 8 * u) : u32x4{0u, 0u, 0u, 0u};
+  }
+  uint32_t b4[4] = {0u, 0u, 0u, 0u}, t4[4] = {0u, 0u, 0u, 0u};  // packed 16-bit digit pairs
+#pragma unroll
+  for (int r = 0; r < kShortMaxTiles / kG; ++r) {
+    const int i = r * kG + g;
+    const uint32_t inb = i < lo ? ~0u : 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      t4[q] += v[r][q];
+      b4[q] += v[r][q] & inb;
+    }
+  }
+  // part[0][g][d] = before, part[1][g][d] = total (16-bit lanes pack two digits)
+  uint32_t* pw = (uint32_t*)part;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    pw[(0 * kG + g) * (kRadix / 2) + 4 * u + q] = b4[q];
+    pw[(1 * kG + g) * (kRadix / 2) + 4 * u + q] = t4[q];
+  }
+  __syncthreads();
+  uint32_t sb = 0, st = 0;
+#pragma unroll
+  for (int gg = 0; gg < kG; ++gg) {
+    sb += part[(0 * kG + gg) * kRadix + tid];
+    st += part[(1 * kG + gg) * kRadix + tid];
+  }
+  *bef = sb;
+  *tot = st;
+  __syncthreads();
+}
+
+// The pass-0 scatter of bucket mode with its offsets computed in place (no
+// offsets kernel): each block reads its segment's pack histograms of the
+// high digit, the segment's blocks all decide the same mode (bucket link when
+// no high-digit bucket exceeds bucket_max keys, else the low digit first and
+// the look-back link), and the tile-0 block publishes the scattered pass's
+// digit bases, the mode and fresh look-back tickets for the link.
+template <typename U, int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
+    const U* __restrict__ in, U* __restrict__ out, const uint16_t* __restrict__ hist, int nt0,
+    int m, int64_t T, int ntiles, int64_t nblk, int tbits, uint32_t* __restrict__ zero0,
+    int64_t zero0_words, uint32_t* __restrict__ binbase, uint32_t* __restrict__ modes,
+    uint32_t* __restrict__ tickets, int npass, int64_t nseg, uint32_t bucket_max) {
+  constexpr int NW = kSortThreads / kWave;
+  constexpr int TILE = kSortThreads * ITEMS;
+  static_assert(TILE * sizeof(U) >= 2 * 8 * kRadix * sizeof(uint16_t), "partial sums in stage");
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ int32_t gbase[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ __align__(16) U stage[TILE];
+  zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
+  const int tid = threadIdx.x;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  const int64_t seg = lb / ntiles;
+  const int tile = (int)(lb - seg * ntiles);
+  const int64_t start = (int64_t)tile * TILE;
+  const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  constexpr int nh = 2;  // histogram passes: the low and the high digit
+  const int per = nh * kRadix;
+  const uint16_t* hs = hist + seg * (int64_t)nt0 * per;
+  U key[ITEMS];
+  load_tile<U, ITEMS>(in + seg * T + start, n, key);
+  uint32_t bef, tot;
+  hist_sums<kSortThreads>(hs + kRadix, per, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
+  const int big = __syncthreads_or(tot > bucket_max);
+  const int mp = big ? 0 : 1;  // the digit this segment scatters by (1 = high)
+  if (!mp) hist_sums<kSortThreads>(hs, per, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
+  const uint32_t base = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
+  if (tile == 0) {
+    binbase[(seg * nh + mp) * kRadix + tid] = base;
+    if (tid == 0) modes[seg] = (uint32_t)mp;
+    if (tid < npass) tickets[(int64_t)tid * nseg + seg] = 0;  // [pass][seg]
+  }
+  const int shift = tbits + 8 * mp;
+  uint32_t rank[ITEMS];
+  uint32_t own;
+  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  gbase[tid] = (int32_t)((int64_t)bef + (int64_t)base - (int64_t)dstart[tid]);
+  __syncthreads();
+  stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
+}
+
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ binbase_p,
@@ -1189,23 +1290,29 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   });
   if (e != hipSuccess) return e;
   // Pass-0 tile offsets and the digit bases of every pass, from the pack
-  // histograms: one block per (segment, pass) for short segments, else one
-  // 1024-thread block per segment.
-  if (nt0 <= kShortMaxTiles) {
+  // histograms: in bucket mode inside the first scatter itself; otherwise one
+  // block per (segment, pass) for short segments, else one 1024-thread block
+  // per segment, before the first scatter.
+  const int64_t nblk0 = tp.nseg() * nsct;
+  const unsigned g0 = xcd_grid(nblk0, 1, (int64_t)1 << 31);
+  uint32_t* next0 = npass > 1 ? status[0] : nullptr;
+  if (bucket) {  // bucket_mode() implies nt0 <= kShortMaxTiles and two passes
+    scatter0_bucket_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
+        ka, kb, hist, nt0, m, tp.T, nsct, nblk0, tp.tbits, next0, status_words, binbase, modes,
+        tickets, npass, tp.nseg(), (uint32_t)(kLinkWaves * kLinkRun));
+  } else if (nt0 <= kShortMaxTiles) {
     const int lm = __builtin_ctz((unsigned)m);
     seg_offsets_kernel<<<(unsigned)(tp.nseg() * nh), kSortThreads, 0, s>>>(
-        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg(), bucket ? 2 : 1, modes,
+        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg(), 1, nullptr,
         (uint32_t)(kLinkWaves * kLinkRun));
   } else {
     scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, nh, npass, offs, nsct,
                                                            binbase, tickets);
   }
-  const int64_t nblk0 = tp.nseg() * nsct;
-  const unsigned g0 = xcd_grid(nblk0, 1, (int64_t)1 << 31);
-  uint32_t* next0 = npass > 1 ? status[0] : nullptr;
-  scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
-      ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words, modes,
-      offs_pass);
+  if (!bucket)
+    scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
+        ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words, nullptr,
+        offs_pass);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (bucket) {
