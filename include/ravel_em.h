@@ -243,10 +243,11 @@ int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, con
  * read, k=1) (zero rows where nothing was written).  The looked-up rows are
  * gathered straight into the GEMM's MFMA tiles and never stored.  read_addr
  * may be null (reads == writes).  payload [B,T,C,P] and weight [M, C*P] are
- * bf16 or f16 (the same dtype); out [B,T,M] is that dtype, accumulated in fp32.
- * Needs P % 8 == 0, M % 8 == 0, M <= 256 and 16-byte aligned payload, weight
- * and out (RAVEL_EM_EINVAL otherwise).  out_src (optional) receives the int32
- * sources [B,T,C] (-1 = zero row) that the backward needs.
+ * bf16, f16 or f32 (the same dtype); out [B,T,M] is that dtype, accumulated in
+ * fp32 (f32: fp32 MFMA products).  Needs P % 8 == 0 for 16-bit payloads,
+ * P % 4 == 0 for f32, and 16-byte aligned payload and weight (RAVEL_EM_EINVAL
+ * otherwise); any M.  out_src (optional) receives the int32 sources [B,T,C]
+ * (-1 = zero row) that the backward needs.
  */
 size_t ravel_em_latest1_linear_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
                                          int has_read, int want_src);

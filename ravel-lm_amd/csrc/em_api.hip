@@ -772,14 +772,14 @@ int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, i
   g_err.clear();
   if (int rc = check_tape(B, T, C, A)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
-  if (payload_dtype != kBF16 && payload_dtype != kF16)
-    return fail(RAVEL_EM_EINVAL, "the fused latest-1 linear takes bf16 or f16 payloads (got %d)",
-                payload_dtype);
+  if (payload_dtype != kBF16 && payload_dtype != kF16 && payload_dtype != kF32)
+    return fail(RAVEL_EM_EINVAL,
+                "the fused latest-1 linear takes bf16, f16 or f32 payloads (got %d)", payload_dtype);
   if (P < 1 || M < 1) return fail(RAVEL_EM_EINVAL, "P and M must be positive");
   if (!gather_gemm_apply(payload_dtype, P, M, payload, weight, out))
     return fail(RAVEL_EM_EINVAL,
-                "the fused latest-1 linear needs P %% 8 == 0, M %% 8 == 0, M <= 256 and 16-byte "
-                "aligned payload, weight and output (P=%lld M=%lld)",
+                "the fused latest-1 linear needs P %% 8 == 0 (16-bit payloads) or P %% 4 == 0 "
+                "(f32) and 16-byte aligned payload and weight (P=%lld M=%lld)",
                 (long long)P, (long long)M);
   if (B * T * C == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !weight || !out) return fail(RAVEL_EM_EINVAL, "null pointer");

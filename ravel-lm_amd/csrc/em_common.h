@@ -256,9 +256,10 @@ hipError_t gather_rows(const void* rows, int64_t nsrc, const int32_t* src, int64
                        int64_t row_bytes, void* out, uint8_t* mask, hipStream_t s,
                        bool once = false);
 // out[n, m] = sum_k A[n, k] W[m, k] with A gathered through record-major k == 1
-// sources (n = b*T + t, k = c*P + p); 16-bit payloads (bf16/f16), W [M][C*P] of
+// sources (n = b*T + t, k = c*P + p); bf16, f16 or f32 payloads, W [M][C*P] of
 // the same dtype, out [NR][M].  gather_gemm_apply says whether the MFMA kernel
-// takes the shape (P % 8 == 0, M % 8 == 0, M <= 256, 16-byte aligned).
+// takes the shape (P a multiple of the values in 16 bytes, payload and W
+// 16-byte aligned; any M).
 bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, const void* W,
                        const void* out);
 hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, int dtype,

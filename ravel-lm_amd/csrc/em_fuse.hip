@@ -11,18 +11,22 @@
 //   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
 //
 // Tiles: a block (8 waves, one block per CU) computes kRows rows x 64*CT
-// columns (CT = ceil(M / 64), so every wave has columns to compute) over K in
-// chunks of kChunk; wave (g, h) owns rows [64g, 64g+64) and columns
+// columns (CT = ceil(M / 64), at most 4; wider M takes more column blocks,
+// grid.y) over K in chunks of 128 bytes of a row (64 bf16/f16 values or 32
+// fp32 values); wave (g, h) owns rows [64g, 64g+64) and columns
 // [16*CT*h, 16*CT*(h+1)).  A chunk's A tile is gathered in 16-byte units (8
-// values; P % 8 == 0 keeps a unit inside one head), W's tile is read
-// row-major, both go to LDS with rows padded to kLds elements (144 bytes: the
-// 16 rows that one MFMA operand read touches land in distinct banks).  A wave
-// runs 4 x CT tiles of v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation,
-// rounded once to the payload dtype.  Operand lane layout (checked on the
-// device): A lane l holds row l%16, k (l/16)*8 .. +7; B lane l holds column
-// l%16, the same k; the result lane l holds column l%16, rows (l/16)*4 .. +3.
-// The epilogue stages the tile in LDS and writes whole 16-byte units of the
-// output rows.
+// 16-bit or 4 fp32 values; P a multiple of that keeps a unit inside one head),
+// W's tile is read row-major, both go to LDS with rows padded to 144 bytes
+// (the 16 rows that one MFMA operand read touches land in distinct banks).  A
+// wave runs 4 x CT tiles of v_mfma_f32_16x16x32_{bf16,f16} per 32 k, or of four
+// v_mfma_f32_16x16x4_f32 per 16 k (fp32 payloads: lane group g's 16-byte unit
+// holds k = 4g .. 4g+3 and the four MFMAs take one each, the same k order for
+// A and B), with fp32 accumulation, rounded once to the payload dtype.
+// Operand lane layout (checked on the device): A lane l holds row l%16 and the
+// k of its unit; B lane l holds column l%16, the same k; the result lane l
+// holds column l%16, rows (l/16)*4 .. +3.  The epilogue stages the tile in LDS
+// and writes whole 16-byte units of the output rows when they are whole units
+// (M a multiple of 8 for 16-bit, of 4 for fp32), else single values.
 //
 // Pipelining: two LDS buffers and two register sets.  While a chunk multiplies
 // out of one LDS buffer, the next chunk (loaded into registers two chunks
@@ -48,8 +52,8 @@ constexpr int kThreads = 512;  // 8 waves: 2 row groups x 4 column groups
 constexpr int kRows = 128;
 constexpr int kSrcLds = 32;  // heads whose sources a block stages in LDS
 constexpr int kCols = 256;   // the widest column tile (CT = 4)
-constexpr int kChunk = 64;
-constexpr int kLds = kChunk + 8;
+constexpr int kChunkBytes = 128;  // of one row per K chunk: 8 units of 16 bytes
+constexpr int kLdsBytes = kChunkBytes + 16;  // padded LDS row
 constexpr int kSets = 2;  // register sets of prefetched chunks (even: LDS parity is static)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -59,43 +63,65 @@ typedef float f32x2v_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2v_t __attribute__((ext_vector_type(2)));
 
-template <bool F16>
-__device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
-  if constexpr (F16)
+// Payload kinds of the kernel: the element type and the MFMA that consumes
+// one 16-byte operand unit per lane.
+enum FuseDt : int { kFuseBF16 = 0, kFuseF16 = 1, kFuseF32 = 2 };
+
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma_unit(u32x4 a, u32x4 b, f32x4_t c) {
+  if constexpr (DT == kFuseF16) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-  else
+  } else if constexpr (DT == kFuseBF16) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[s]), __uint_as_float(b[s]), c, 0,
+                                               0, 0);
+    return c;
+  }
 }
 
-template <bool F16>
-__device__ __forceinline__ uint16_t round16(float x) {
-  const f32x2v_t v = {x, 0.0f};
-  if constexpr (F16)
-    return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2v_t));
-  else
-    return (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
+// One accumulator value in the output dtype (16-bit kinds: rounded once).
+template <int DT>
+__device__ __forceinline__ void put_out(void* base, int64_t i, float x) {
+  if constexpr (DT == kFuseF32) {
+    ((float*)base)[i] = x;
+  } else {
+    const f32x2v_t v = {x, 0.0f};
+    uint16_t h;
+    if constexpr (DT == kFuseF16)
+      h = (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2v_t));
+    else
+      h = (uint16_t)__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v_t));
+    ((uint16_t*)base)[i] = h;
+  }
 }
 
 __device__ u32x4 kZeroUnit = {0u, 0u, 0u, 0u};  // never written: the unit a missing row reads
 
-template <bool F16, bool SRC_LDS, int CT>
+template <int DT, bool SRC_LDS, int CT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gather_gemm_kernel(
-    const uint16_t* __restrict__ payload, const int32_t* __restrict__ src,
-    const uint16_t* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
-    uint16_t* __restrict__ out) {
+    const unsigned char* __restrict__ payload, const int32_t* __restrict__ src,
+    const unsigned char* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
+    unsigned char* __restrict__ out) {
+  constexpr int ES = DT == kFuseF32 ? 4 : 2;  // element bytes
+  constexpr int VPU = 16 / ES;                // values per 16-byte unit
+  constexpr int KCH = kChunkBytes / ES;       // k per chunk
   constexpr int RT = 4;             // 16-row tiles per wave (64 rows)
   constexpr int BC = 64 * CT;       // columns of the block
   constexpr int AU = kRows * 8 / kThreads;
   constexpr int BU = BC * 8 / kThreads;
   static_assert(BU * kThreads == BC * 8, "whole W units per thread");
-  __shared__ __align__(16) uint16_t As[2][kRows * kLds];
-  __shared__ __align__(16) uint16_t Bs[2][BC * kLds];
+  __shared__ __align__(16) unsigned char As[2][kRows * kLdsBytes];
+  __shared__ __align__(16) unsigned char Bs[2][BC * kLdsBytes];
   __shared__ int32_t Ss[kRows * kSrcLds];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wrow = wave >> 2, wcol = wave & 3;  // 64-row group, column group
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
+  const int col0 = (int)blockIdx.y * BC;  // the block's first output column
   const int K = C * P;
   // The block's sources [kRows][C] (one contiguous run) go to LDS once, so a
   // chunk's gather costs one memory round trip.
@@ -112,12 +138,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   u32x4 av[kSets][AU], bv[kSets][BU];
   const u32x4* zero = &kZeroUnit;
   auto load_chunk = [&](int ch, u32x4 (&a)[AU], u32x4 (&bb)[BU]) {
-    const int k0 = ch * kChunk;
+    const int k0 = ch * KCH;
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
       const int u = tid + kThreads * q;
       const int r = u >> 3, piece = u & 7;
-      const int k = k0 + piece * 8;
+      const int k = k0 + piece * VPU;
       const int64_t n = row0 + r;
       // Branch-free: an out-of-range or missing row reads a zero unit.
       const bool in = n < NR && k < K;
@@ -125,42 +151,44 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int c = (int)fdiv((uint32_t)kc, byP);
       const int32_t s = SRC_LDS ? Ss[r * C + c] : src[(in ? n : row0) * C + c];
       const bool ok = in && s >= 0 && s < nsrc;
-      a[q] = *(ok ? (const u32x4*)(payload + (int64_t)s * P + (kc - c * P)) : zero);
+      a[q] = *(ok ? (const u32x4*)(payload + ((int64_t)s * P + (kc - c * P)) * ES) : zero);
     }
 #pragma unroll
     for (int q = 0; q < BU; ++q) {
       const int u = tid + kThreads * q;
-      const int m = u >> 3, piece = u & 7;
-      const int k = k0 + piece * 8;
+      const int m = col0 + (u >> 3), piece = u & 7;
+      const int k = k0 + piece * VPU;
       const bool in = m < M && k < K;
-      bb[q] = *(in ? (const u32x4*)(W + (int64_t)m * K + k) : zero);
+      bb[q] = *(in ? (const u32x4*)(W + ((int64_t)m * K + k) * ES) : zero);
     }
   };
   auto store_chunk = [&](int buf, const u32x4 (&a)[AU], const u32x4 (&bb)[BU]) {
 #pragma unroll
     for (int q = 0; q < AU; ++q) {
       const int u = tid + kThreads * q;
-      *(u32x4*)&As[buf][(u >> 3) * kLds + (u & 7) * 8] = a[q];
+      *(u32x4*)&As[buf][(u >> 3) * kLdsBytes + (u & 7) * 16] = a[q];
     }
 #pragma unroll
     for (int q = 0; q < BU; ++q) {
       const int u = tid + kThreads * q;
-      *(u32x4*)&Bs[buf][(u >> 3) * kLds + (u & 7) * 8] = bb[q];
+      *(u32x4*)&Bs[buf][(u >> 3) * kLdsBytes + (u & 7) * 16] = bb[q];
     }
   };
   auto multiply = [&](int buf) {
+    // two operand units per row per chunk: lane group g reads bytes
+    // [16g, 16g + 16) of each 64-byte half
 #pragma unroll
-    for (int ks = 0; ks < kChunk / 32; ++ks) {
-      const int kk = ks * 32 + (lane >> 4) * 8;
+    for (int ks = 0; ks < 2; ++ks) {
+      const int kb = ks * 64 + (lane >> 4) * 16;
       u32x4 b[CT];
 #pragma unroll
       for (int j = 0; j < CT; ++j)
-        b[j] = *(const u32x4*)&Bs[buf][(wcol * 16 * CT + j * 16 + (lane & 15)) * kLds + kk];
+        b[j] = *(const u32x4*)&Bs[buf][(wcol * 16 * CT + j * 16 + (lane & 15)) * kLdsBytes + kb];
 #pragma unroll
       for (int i = 0; i < RT; ++i) {
-        const u32x4 a = *(const u32x4*)&As[buf][(wrow * 64 + i * 16 + (lane & 15)) * kLds + kk];
+        const u32x4 a = *(const u32x4*)&As[buf][(wrow * 64 + i * 16 + (lane & 15)) * kLdsBytes + kb];
 #pragma unroll
-        for (int j = 0; j < CT; ++j) acc[i][j] = mfma16<F16>(a, b[j], acc[i][j]);
+        for (int j = 0; j < CT; ++j) acc[i][j] = mfma_unit<DT>(a, b[j], acc[i][j]);
       }
     }
   };
@@ -168,7 +196,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // units), so the loop body is straight-line; loads past the last chunk
   // re-read it.  Chunk c multiplies out of LDS buffer c % 2 while chunk c + 1
   // waits in register set (c + 1) % kSets, loaded kSets - 1 chunks earlier.
-  const int nch = (K + kChunk - 1) / kChunk;
+  const int nch = (K + KCH - 1) / KCH;
   const int nchp = (nch + kSets - 1) / kSets * kSets;
   auto clampc = [&](int ch) { return ch < nchp ? ch : nchp - 1; };
 #pragma unroll
@@ -186,12 +214,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       __syncthreads();
     }
   }
-  // Epilogue: round to 16 bits and stage the tile in the (now free) B
-  // buffers, kRows/2 rows at a time (padded rows of BC + 8), then write
-  // 16-byte units.
-  uint16_t* Cs = &Bs[0][0];
-  constexpr int CSTRIDE = BC + 8;
-  static_assert(kRows / 2 * CSTRIDE <= 2 * BC * kLds, "epilogue half-tile must fit the B buffers");
+  // Epilogue: the tile in the output dtype, staged in the (now free) B
+  // buffers kRows/2 rows at a time (padded rows of BC + 16/ES values), then
+  // written in 16-byte units when output rows are whole units, else value by
+  // value.
+  unsigned char* Cs = &Bs[0][0];
+  constexpr int CSTRIDE = BC + VPU;  // values
+  static_assert(kRows / 2 * CSTRIDE * ES <= 2 * BC * kLdsBytes,
+                "epilogue half-tile must fit the B buffers");
+  const int ncol = (M - col0) < BC ? (M - col0) : BC;  // valid columns of the block
+  const bool units = (M % VPU) == 0 && ((uintptr_t)out & 15) == 0;
   // Half h holds the rows of row group h.
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
@@ -204,15 +236,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           for (int e = 0; e < 4; ++e) {
             const int r = i * 16 + (lane >> 4) * 4 + e;
             const int col = wcol * 16 * CT + j * 16 + (lane & 15);
-            Cs[r * CSTRIDE + col] = round16<F16>(acc[i][j][e]);
+            put_out<DT>(Cs, (int64_t)r * CSTRIDE + col, acc[i][j][e]);
           }
     }
     __syncthreads();
-    const int upr = M >> 3;  // 16-byte units per output row (M % 8 == 0)
-    for (int u = tid; u < (kRows / 2) * upr; u += kThreads) {
-      const int r = u / upr, piece = u - (u / upr) * upr;
-      const int64_t n = row0 + half * (kRows / 2) + r;
-      if (n < NR) *(u32x4*)(out + n * M + piece * 8) = *(const u32x4*)&Cs[r * CSTRIDE + piece * 8];
+    if (units) {
+      const int upr = ncol / VPU;  // 16-byte units of the block's part of an output row
+      for (int u = tid; u < (kRows / 2) * upr; u += kThreads) {
+        const int r = u / upr, piece = u - (u / upr) * upr;
+        const int64_t n = row0 + half * (kRows / 2) + r;
+        if (n < NR)
+          *(u32x4*)(out + (n * M + col0 + piece * VPU) * ES) =
+              *(const u32x4*)&Cs[((int64_t)r * CSTRIDE + piece * VPU) * ES];
+      }
+    } else {
+      for (int u = tid; u < (kRows / 2) * ncol; u += kThreads) {
+        const int r = u / ncol, col = u - (u / ncol) * ncol;
+        const int64_t n = row0 + half * (kRows / 2) + r;
+        if (n < NR) {
+          if constexpr (ES == 4)
+            ((float*)out)[n * M + col0 + col] = ((const float*)Cs)[r * CSTRIDE + col];
+          else
+            ((uint16_t*)out)[n * M + col0 + col] = ((const uint16_t*)Cs)[r * CSTRIDE + col];
+        }
+      }
     }
     __syncthreads();
   }
@@ -222,24 +269,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, const void* W,
                        const void* out) {
-  return (dtype == kBF16 || dtype == kF16) && P % 8 == 0 && M >= 8 && M <= kCols && M % 8 == 0 &&
-         (((uintptr_t)payload | (uintptr_t)W | (uintptr_t)out) & 15) == 0;
+  (void)out;  // any alignment: rows that are not whole 16-byte units are written value by value
+  const int64_t vpu = dtype == kF32 ? 4 : 8;
+  return (dtype == kBF16 || dtype == kF16 || dtype == kF32) && P % vpu == 0 && M >= 1 &&
+         (((uintptr_t)payload | (uintptr_t)W) & 15) == 0;
 }
 
 hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, int dtype,
                        int64_t NR, int64_t C, int64_t P, int64_t M, void* out, hipStream_t s) {
   if (NR == 0) return hipSuccess;
   const int64_t blocks = (NR + kRows - 1) / kRows;
-  if (blocks > INT32_MAX || C * P > INT32_MAX) return hipErrorInvalidValue;
+  if (blocks > INT32_MAX || C * P > INT32_MAX || M > INT32_MAX) return hipErrorInvalidValue;
   const int64_t nsrc = NR * C;
   const FastDiv byP = make_fastdiv((uint32_t)P);
-  const int ct = (int)((M + 63) / 64);  // 16-column tiles per wave: ceil(M / 64)
-  auto go = [&](auto f16, auto src_lds) {
-    constexpr bool F = decltype(f16)::value, SL = decltype(src_lds)::value;
-#define REM_GG(CT)                                                                              \
-  gather_gemm_kernel<F, SL, CT><<<(unsigned)blocks, kThreads, 0, s>>>(                           \
-      (const uint16_t*)payload, src, (const uint16_t*)W, NR, (int)C, (int)P, byP, (int)M, nsrc, \
-      (uint16_t*)out)
+  // 16-column tiles per wave: ceil(M / 64) up to 4; wider outputs take
+  // ceil(M / 256) column blocks
+  const int ct = M >= kCols ? 4 : (int)((M + 63) / 64);
+  const int64_t ncb = (M + 64 * ct - 1) / (64 * ct);
+  if (ncb > 65535) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks, (unsigned)ncb);
+  auto go = [&](auto dt, auto src_lds) {
+    constexpr int D = decltype(dt)::value;
+    constexpr bool SL = decltype(src_lds)::value;
+#define REM_GG(CT)                                                                        \
+  gather_gemm_kernel<D, SL, CT><<<grid, kThreads, 0, s>>>(                                 \
+      (const unsigned char*)payload, src, (const unsigned char*)W, NR, (int)C, (int)P, byP, \
+      (int)M, nsrc, (unsigned char*)out)
     switch (ct) {
       case 1: REM_GG(1); break;
       case 2: REM_GG(2); break;
@@ -248,13 +303,18 @@ hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, i
     }
 #undef REM_GG
   };
-  using T_ = std::true_type;
-  using F_ = std::false_type;
-  if (dtype == kF16) {
-    if (C <= kSrcLds) go(T_{}, T_{}); else go(T_{}, F_{});
-  } else {
-    if (C <= kSrcLds) go(F_{}, T_{}); else go(F_{}, F_{});
-  }
+  auto by_src = [&](auto dt) {
+    if (C <= kSrcLds)
+      go(dt, std::true_type{});
+    else
+      go(dt, std::false_type{});
+  };
+  if (dtype == kF16)
+    by_src(std::integral_constant<int, kFuseF16>{});
+  else if (dtype == kF32)
+    by_src(std::integral_constant<int, kFuseF32>{});
+  else
+    by_src(std::integral_constant<int, kFuseBF16>{});
   return hipGetLastError();
 }
 

@@ -10,9 +10,10 @@ mask:
 
 with ``values`` the latest-1 lookup.  On the device the looked-up rows are
 gathered straight into the MFMA tiles of the GEMM (``ravel_em_latest1_linear_fwd``)
-and never stored.  Shapes the MFMA kernel does not take (payloads other than
-bf16/f16, P % 8 != 0, M % 8 != 0, M > 256) run the lookup kernels followed by a
-library GEMM on the device.  There is no CPU path.
+and never stored: bf16/f16 payloads with P % 8 == 0 and f32 payloads with
+P % 4 == 0 (the reference model runs fp32 when autocast is off), any M.  Other
+shapes (f64 payloads, other P, a weight of another dtype) run the lookup kernels
+followed by a library GEMM on the device.  There is no CPU path.
 """
 from __future__ import annotations
 
@@ -28,11 +29,14 @@ Tensor = torch.Tensor
 
 
 def _mfma_ok(payloads: Tensor, weight: Tensor) -> bool:
+    """The MFMA kernel takes bf16/f16 payloads with P % 8 == 0 and f32 payloads
+    with P % 4 == 0 (16-byte units of a head's row), weight of the payload
+    dtype, both 16-byte aligned; any M."""
     P = payloads.shape[-1]
-    M = weight.shape[0]
     aligned = all(t.data_ptr() % 16 == 0 for t in (payloads, weight))
-    return (payloads.dtype in (torch.bfloat16, torch.float16) and P % 8 == 0 and M % 8 == 0
-            and 8 <= M <= 256 and aligned)
+    per_unit = {torch.bfloat16: 8, torch.float16: 8, torch.float32: 4}.get(payloads.dtype)
+    return (per_unit is not None and P % per_unit == 0 and weight.dtype == payloads.dtype
+            and weight.shape[0] >= 1 and aligned)
 
 
 @torch.library.custom_op("ravel_em::latest1_linear", mutates_args=())
