@@ -111,7 +111,8 @@ int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64
 /*
  * Status word of a call.  Every entry point that takes a workspace and sorts
  * (sort_order, latest_k_fwd, latest_k_resolve, latest1_linear_fwd,
- * seg_sum_fwd, seg_sum_bwd, cache_prefill) reserves the first
+ * seg_sum_fwd, seg_sum_bwd, cache_prefill, and latest_k_bwd with chain = 0)
+ * reserves the first
  * RAVEL_EM_STATUS_BYTES of its workspace for a header whose uint32 at offset 0
  * is the call's status word.  The call clears it on `stream` before any other
  * of its kernels runs, and a bounded device-side wait (the look-back of a sort
@@ -260,8 +261,11 @@ int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, i
 /*
  * Backward of causal_last_k_lookup (autograd of ravel_memory.py:173-175;
  * GPU arm triton_latest1.py:132-142): grad_payload[src] += grad_values.
- * `chain` = 1 selects the deterministic successor-chain kernel, valid only when
- * the forward had read == write and no write_mask.
+ * Deterministic (bit-identical across runs) in both forms: `chain` = 1 is the
+ * successor-chain kernel, valid only when the forward had read == write and no
+ * write_mask; `chain` = 0 takes any sources (separate reads, masks) and sums
+ * each source's slots in slot order after a stable sort of the source ids
+ * (its workspace carries a status word, as the sorting entry points' do).
  */
 size_t ravel_em_latest_k_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k,
                                        int payload_dtype, int chain);

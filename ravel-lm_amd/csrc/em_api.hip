@@ -489,6 +489,38 @@ __global__ void copy_word_kernel(const uint32_t* __restrict__ src, uint32_t* __r
   if (threadIdx.x == 0) *dst = *src;
 }
 
+// ----------------------------------------------- latest-k backward (sorted) --
+// grad_payload[s] = sum of grad_values[r, j] over the slots with src[r, j] = s
+// (the index_add_ that autograd makes of ravel_lm/ravel_memory.py:173-174),
+// deterministic: the slots' source ids are sorted as one tape of N*k keys
+// (stable, so each run lists its slots in slot order; empty slots, -1, sort
+// last) and each run's rows are summed in that order by the segmented-sum
+// kernels, which write the total to row s.  Records no slot names stay zero.
+Tape bwd_tape(int64_t N, int64_t k) { return make_tape(1, N * k, 1, N > 0 ? N : 1, true, kNegLast); }
+
+template <typename U>
+int latest_k_bwd_sorted(const int32_t* src, const void* grad_values, int dtype, int64_t N,
+                        int64_t D, int64_t k, void* grad_payload, void* ws, size_t wsb,
+                        hipStream_t s) {
+  Bump bp(ws);
+  Tape tp = bwd_tape(N, k);
+  SumWs<U> w = take_sum<U>(bp, tp, D, dtype, true, false);
+  tp.status = w.sw.status;
+  if (int rc = check_ws(bp, wsb)) return rc;
+  hipError_t e = fill_bytes(grad_payload, 0, (size_t)(N * D) * (size_t)dtype_size(dtype), s);
+  if (e != hipSuccess) return hip_fail(e, "latest-k backward");
+  AddrIn ids;
+  ids.kind = kI32;
+  ids.dense = src;
+  U* sorted = nullptr;
+  e = sort_call<U>(ids, nullptr, tp, w.sw, &sorted, s, (uint32_t*)w.walk, 2 * w.walk_words);
+  if (e != hipSuccess) return hip_fail(e, "latest-k backward sort");
+  e = run_totals<U>(sorted, grad_values, dtype, tp, D, N, grad_payload, w.tail, w.flag, w.carry,
+                    w.walk, s);
+  if (e != hipSuccess) return hip_fail(e, "latest-k backward sums");
+  return RAVEL_EM_OK;
+}
+
 }  // namespace
 
 void stage_begin(int stage, hipStream_t s) {
@@ -823,14 +855,17 @@ int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, con
 
 size_t ravel_em_latest_k_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k,
                                        int payload_dtype, int chain) {
-  (void)k;
-  Bump bp(nullptr);
+  if (check_tape(B, T, C, 1) || k < 1 || D < 1) return 0;
   const int64_t N = B * T * C;
-  if (chain)
+  if (chain) {
+    Bump bp(nullptr);
     bp.take<int32_t>((size_t)N);
-  else if (payload_dtype == kBF16 || payload_dtype == kF16)
-    bp.take<float>((size_t)(N * D));
-  return bp.off;
+    return bp.off;
+  }
+  if (N * k > kMaxRecords) return 0;
+  const Tape tp = bwd_tape(N, k);
+  return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, true, false)
+                   : sum_ws_t<uint32_t>(tp, D, payload_dtype, true, false);
 }
 
 int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int payload_dtype,
@@ -842,23 +877,24 @@ int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int paylo
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (k < 1 || D < 1) return fail(RAVEL_EM_EINVAL, "k and D must be positive");
   const int64_t N = B * T * C;
-  if (N == 0) return RAVEL_EM_OK;
+  if (N == 0) return chain ? RAVEL_EM_OK : clear_status(workspace, workspace_bytes, stream);
   if (!src || !grad_values || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
-  Bump bp(workspace);
-  int32_t* next = nullptr;
-  float* acc = nullptr;
-  if (chain)
-    next = bp.take<int32_t>((size_t)N);
-  else if (payload_dtype == kBF16 || payload_dtype == kF16)
-    acc = bp.take<float>((size_t)(N * D));
-  if (int rc = check_ws(bp, workspace_bytes)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = chain ? latest_k_bwd_chain(src, grad_values, payload_dtype, N, D, (int)k, next,
-                                            grad_payload, s)
-                       : latest_k_bwd_atomic(src, grad_values, payload_dtype, N, D, (int)k, acc,
-                                             grad_payload, s);
-  if (e != hipSuccess) return hip_fail(e, "latest-k backward");
-  return RAVEL_EM_OK;
+  if (chain) {
+    Bump bp(workspace);
+    int32_t* next = bp.take<int32_t>((size_t)N);
+    if (int rc = check_ws(bp, workspace_bytes)) return rc;
+    hipError_t e = latest_k_bwd_chain(src, grad_values, payload_dtype, N, D, (int)k, next,
+                                      grad_payload, s);
+    if (e != hipSuccess) return hip_fail(e, "latest-k backward");
+    return RAVEL_EM_OK;
+  }
+  if (N * k > kMaxRecords) return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
+  return bwd_tape(N, k).wide()
+             ? latest_k_bwd_sorted<uint64_t>(src, grad_values, payload_dtype, N, D, k,
+                                             grad_payload, workspace, workspace_bytes, s)
+             : latest_k_bwd_sorted<uint32_t>(src, grad_values, payload_dtype, N, D, k,
+                                             grad_payload, workspace, workspace_bytes, s);
 }
 
 size_t ravel_em_seg_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,

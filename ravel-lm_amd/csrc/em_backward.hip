@@ -9,8 +9,9 @@
 //           reader's slot-0 successor, and so on.  next[src[r,0]] = r builds the
 //           chain without collisions, and each gradient row is summed in slot
 //           order j = 0..k-1: deterministic, no atomics.
-//   atomic  separate reads or masked writes: hardware fp32/fp64 atomics into an
-//           accumulator, then one conversion pass to the payload dtype.
+//   sorted  separate reads or masked writes: the slots' source ids are sorted
+//           and each source's slots summed in slot order by the segmented-sum
+//           kernels (em_api.hip, latest_k_bwd_sorted): deterministic too.
 
 #include "em_common.h"
 #include "em_elem.h"
@@ -56,28 +57,6 @@ __global__ __launch_bounds__(256) void chain_grad_kernel(
   }
 }
 
-template <int DT, typename G>
-__global__ __launch_bounds__(256) void atomic_grad_kernel(
-    const int32_t* __restrict__ src, const typename Elem<DT>::store_t* __restrict__ gv,
-    int64_t rows, int64_t D, int64_t nsrc, G* __restrict__ acc) {
-  const int64_t total = rows * D;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = e / D;
-    const int64_t col = e - row * D;
-    const int32_t s = src[row];
-    if (s >= 0 && s < nsrc) unsafeAtomicAdd(&acc[(int64_t)s * D + col], (G)Elem<DT>::load(gv[e]));
-  }
-}
-
-template <int DT, typename G>
-__global__ __launch_bounds__(256) void convert_kernel(const G* __restrict__ acc, int64_t n,
-                                                     typename Elem<DT>::store_t* __restrict__ out) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    out[i] = Elem<DT>::store((typename Elem<DT>::acc_t)acc[i]);
-}
-
 template <int DT>
 hipError_t chain_t(const int32_t* src, const void* gv, int64_t N, int64_t D, int k, int32_t* next,
                    void* gp, hipStream_t s) {
@@ -85,21 +64,6 @@ hipError_t chain_t(const int32_t* src, const void* gv, int64_t N, int64_t D, int
   fill_i32_kernel<<<grid_for(N, 256), 256, 0, s>>>(next, N, -1);
   next_chain_kernel<<<grid_for(N, 256), 256, 0, s>>>(src, N, k, next);
   chain_grad_kernel<DT><<<grid_for(N * D, 256), 256, 0, s>>>(next, (const S*)gv, N, D, k, (S*)gp);
-  return hipGetLastError();
-}
-
-template <int DT>
-hipError_t atomic_t(const int32_t* src, const void* gv, int64_t N, int64_t D, int k, float* accw,
-                    void* gp, hipStream_t s) {
-  using S = typename Elem<DT>::store_t;
-  using G = typename std::conditional<DT == kF64, double, float>::type;
-  G* acc = (DT == kF32 || DT == kF64) ? (G*)gp : (G*)accw;
-  hipError_t e = fill_bytes(acc, 0, (size_t)(N * D) * sizeof(G), s);
-  if (e != hipSuccess) return e;
-  atomic_grad_kernel<DT, G><<<grid_for(N * k * D, 256), 256, 0, s>>>(src, (const S*)gv, N * k, D,
-                                                                      N, acc);
-  if (!(DT == kF32 || DT == kF64))
-    convert_kernel<DT, G><<<grid_for(N * D, 256), 256, 0, s>>>(acc, N * D, (S*)gp);
   return hipGetLastError();
 }
 
@@ -112,17 +76,6 @@ hipError_t latest_k_bwd_chain(const int32_t* src, const void* grad_values, int d
     case kF64: return chain_t<kF64>(src, grad_values, N, D, k, next, grad_payload, s);
     case kBF16: return chain_t<kBF16>(src, grad_values, N, D, k, next, grad_payload, s);
     case kF16: return chain_t<kF16>(src, grad_values, N, D, k, next, grad_payload, s);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-hipError_t latest_k_bwd_atomic(const int32_t* src, const void* grad_values, int dtype, int64_t N,
-                               int64_t D, int k, float* acc, void* grad_payload, hipStream_t s) {
-  switch (dtype) {
-    case kF32: return atomic_t<kF32>(src, grad_values, N, D, k, acc, grad_payload, s);
-    case kF64: return atomic_t<kF64>(src, grad_values, N, D, k, acc, grad_payload, s);
-    case kBF16: return atomic_t<kBF16>(src, grad_values, N, D, k, acc, grad_payload, s);
-    case kF16: return atomic_t<kF16>(src, grad_values, N, D, k, acc, grad_payload, s);
     default: return hipErrorInvalidValue;
   }
 }

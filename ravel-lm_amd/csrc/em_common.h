@@ -25,7 +25,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Address reduction modes: the lookups wrap with Python remainder
 // (ravel_memory.py:127-128), the decode cache clamps (ravel_memory.py:276,289).
-enum AddrMode : int { kWrap = 0, kClamp = 1 };
+// kNegLast sorts values already in [0, A) as they are and negative ones at the
+// sentinel A, last (the backward's sort of source record ids, -1 = none).
+enum AddrMode : int { kWrap = 0, kClamp = 1, kNegLast = 2 };
 
 // Host-side description of one event tape.
 struct Tape {
@@ -158,6 +160,7 @@ __device__ __forceinline__ uint32_t count_below(uint64_t mask) {
 
 __device__ __forceinline__ int64_t reduce_addr(int64_t a, int64_t A, int mode, bool trunc32) {
   if (mode == kClamp) return a < 0 ? 0 : (a >= A ? A - 1 : a);
+  if (mode == kNegLast) return a < 0 ? A : a;
   if (trunc32) a = (int64_t)(int32_t)(uint32_t)(uint64_t)a;
   if ((uint64_t)a < (uint64_t)A) return a;
   const int64_t r = a % A;
@@ -284,12 +287,18 @@ hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& 
 size_t seg_sum_chunks(const Tape& tp);
 size_t acc_bytes(int dtype);
 size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype);
+// Totals of runs: out[a] = sum of rows[r] over the records r of the run of
+// address a in the sorted tape (rows indexed by record, accumulated in fp32 for
+// 16-bit rows and fp64 otherwise, rounded once), for every run with a < nout;
+// other out rows are left as they are.  Same workspace as seg_sum.
+template <typename U>
+hipError_t run_totals(const U* sorted, const void* rows, int dtype, const Tape& tp, int64_t D,
+                      int64_t nout, void* out, void* tail, uint8_t* flag, void* carry,
+                      uint64_t* walk, hipStream_t s);
 
 // Backward of latest-k: grad_payload[src[r,j]] += grad_values[r,j].
 hipError_t latest_k_bwd_chain(const int32_t* src, const void* grad_values, int dtype, int64_t N,
                               int64_t D, int k, int32_t* next, void* grad_payload, hipStream_t s);
-hipError_t latest_k_bwd_atomic(const int32_t* src, const void* grad_values, int dtype, int64_t N,
-                               int64_t D, int k, float* acc, void* grad_payload, hipStream_t s);
 
 template <typename U>
 hipError_t seg_sum_bwd(const U* sorted, const int32_t* spos, const void* grad_out, int dtype,

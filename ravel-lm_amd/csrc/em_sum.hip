@@ -22,6 +22,9 @@
 //   INCL       inclusive sum (else exclusive)
 //   OUT_SORTED output row = sorted position (else: original record index)
 //   WMASK      also write the per-record "has an earlier record" mask
+//   RT         run totals: only the last position of each run writes, its
+//              inclusive sum, to output row = the run's address (addresses at
+//              or past nout are skipped)
 
 #include "em_common.h"
 #include "em_elem.h"
@@ -63,7 +66,9 @@ struct ChunkView {
   int n;           // positions in this chunk
   int64_t pos;     // this lane's sorted position inside the segment
   int64_t rec;     // this lane's original record index
+  int64_t addr;    // this lane's address (-2 past the chunk)
   uint64_t smask;  // run starts in walk order
+  bool last_end;   // (end_of_chunk() only) the chunk's last position ends its run
   __device__ __forceinline__ void init(const U* __restrict__ sorted, int64_t chunk, int64_t nch_seg,
                                        int64_t T, int64_t C, int tbits) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -90,21 +95,31 @@ struct ChunkView {
       }
     }
     rec = valid ? ((b * T + (int64_t)(u & tmask)) * C + c) : 0;
+    addr = a;
     smask = __ballot(valid && a != ap);
+  }
+  // Whether the record after the chunk starts a new run (or the segment ends).
+  __device__ __forceinline__ void end_of_chunk(const U* __restrict__ sorted, int64_t T, int tbits) {
+    const int64_t wn = i0 + n;  // walk index after the chunk
+    const int64_t alast = readlane64(addr, n - 1);
+    bool e = true;
+    if (wn < T) e = (int64_t)(sorted[seg * T + (REV ? (T - 1 - wn) : wn)] >> tbits) != alast;
+    last_end = e;
   }
 };
 
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT>
 __global__ __launch_bounds__(256) void segsum_local_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int64_t nch_seg, int64_t nchunks, XOut* __restrict__ out,
-    uint8_t* __restrict__ omask, Acc* __restrict__ tail, uint8_t* __restrict__ flag) {
+    uint8_t* __restrict__ omask, Acc* __restrict__ tail, uint8_t* __restrict__ flag, int64_t nout) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t chunk = (int64_t)blockIdx.x * (256 / kWave) + (threadIdx.x / kWave);
   if (chunk >= nchunks) return;
   ChunkView<U, REV> cv;
   cv.init(sorted, chunk, nch_seg, T, C, tbits);
+  if (RT) cv.end_of_chunk(sorted, T, tbits);
   const int64_t col = (int64_t)blockIdx.y * kWave + lane;
   const bool colok = col < D;
   const int64_t segbase = cv.seg * T;
@@ -135,7 +150,11 @@ __global__ __launch_bounds__(256) void segsum_local_kernel(
         if (WMASK && lane == 0 && blockIdx.y == 0) omask[orow] = st ? 0 : 1;
       }
       acc += LoadF::load(v[i]);
-      if (INCL && seen) {
+      if (RT) {
+        const bool last = (i + 1 < cv.n) ? ((cv.smask >> (i + 1)) & 1ull) != 0 : cv.last_end;
+        const int64_t a = readlane64(cv.addr, i);
+        if (seen && last && a >= 0 && a < nout && colok) out[a * D + col] = StoreF::store(acc);
+      } else if (INCL && seen) {
         if (colok) out[orow * D + col] = StoreF::store(acc);
         if (WMASK && lane == 0 && blockIdx.y == 0) omask[orow] = 1;
       }
@@ -187,11 +206,11 @@ __global__ __launch_bounds__(1024) void segsum_carry_kernel(const Acc* __restric
 }
 
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT>
 __global__ __launch_bounds__(256) void segsum_fixup_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int64_t nch_seg, int64_t nchunks, XOut* __restrict__ out,
-    uint8_t* __restrict__ omask, const Acc* __restrict__ carry) {
+    uint8_t* __restrict__ omask, const Acc* __restrict__ carry, int64_t nout) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t chunk = (int64_t)blockIdx.x * (256 / kWave) + (threadIdx.x / kWave);
   if (chunk >= nchunks) return;
@@ -199,6 +218,7 @@ __global__ __launch_bounds__(256) void segsum_fixup_kernel(
   cv.init(sorted, chunk, nch_seg, T, C, tbits);
   const int lead = cv.smask ? (int)__builtin_ctzll(cv.smask) : cv.n;
   if (lead == 0) return;
+  if (RT) cv.end_of_chunk(sorted, T, tbits);
   const int64_t col = (int64_t)blockIdx.y * kWave + lane;
   const bool colok = col < D;
   const int64_t segbase = cv.seg * T;
@@ -211,7 +231,12 @@ __global__ __launch_bounds__(256) void segsum_fixup_kernel(
       if (WMASK && lane == 0 && blockIdx.y == 0) omask[orow] = 1;
     }
     if (colok) acc += LoadF::load(in[irow * D + col]);
-    if (INCL) {
+    if (RT) {
+      // the leading run ends inside the chunk, or at its end
+      const bool last = i + 1 == lead && (lead < cv.n || cv.last_end);
+      const int64_t a = readlane64(cv.addr, i);
+      if (last && a >= 0 && a < nout && colok) out[a * D + col] = StoreF::store(acc);
+    } else if (INCL) {
       if (colok) out[orow * D + col] = StoreF::store(acc);
       if (WMASK && lane == 0 && blockIdx.y == 0) omask[orow] = 1;
     }
@@ -328,11 +353,12 @@ __device__ __forceinline__ void add_unit(Acc* acc, u32x4 x) {
 }
 
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT>
 __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int G, int64_t nparts, XOut* __restrict__ out, uint8_t* __restrict__ omask,
-    uint64_t* __restrict__ status, uint64_t* __restrict__ tickets, uint32_t* __restrict__ err) {
+    uint64_t* __restrict__ status, uint64_t* __restrict__ tickets, uint32_t* __restrict__ err,
+    int64_t nout) {
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
   using OutV = typename Unit<CPU * (int)sizeof(XOut)>::T;
   constexpr int NWMAX = kWalkThreads;  // walkers when G == 1
@@ -376,8 +402,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     }
     st[i] = start ? 1 : 0;
   }
-  if (SKIP_LAST && tid == 0)
-    s_next = (p0 + n >= T || (sk[p0 + n] >> tbits) != (kk[n - 1] >> tbits)) ? 1 : 0;
+  if ((SKIP_LAST || RT) && tid == 0) {
+    const int64_t wn = p0 + n;  // walk index after the part
+    s_next = (wn >= T || (sk[REV ? (T - 1 - wn) : wn] >> tbits) != (kk[n - 1] >> tbits)) ? 1 : 0;
+  }
   __syncthreads();
   auto needed = [&](int i) -> bool {  // row i feeds a later output of its run
     return !SKIP_LAST || ((i + 1 < n) ? st[i + 1] == 0 : s_next == 0);
@@ -492,7 +520,14 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
         const int64_t orw = orow(i);
         if (!INCL) __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[orw * G]);
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
-        if (INCL) __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[orw * G]);
+        if (RT) {
+          const bool last = (i + 1 < n) ? st[i + 1] != 0 : s_next != 0;
+          const int64_t a = (int64_t)(kk[i] >> tbits);
+          if (last && a < nout)
+            __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[a * G]);
+        } else if (INCL) {
+          __builtin_nontemporal_store(pack_unit<XOut, StoreF, Acc, CPU>(acc), &ou[orw * G]);
+        }
         if (WMASK && v == 0) omask[orw] = start ? 0 : 1;
       }
     }
@@ -500,10 +535,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 }
 
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT = false>
 hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D, XOut* out,
                       uint8_t* omask, Acc* tail, uint8_t* flag, Acc* carry, uint64_t* walk,
-                      hipStream_t s) {
+                      hipStream_t s, int64_t nout = 0) {
   const int64_t in_bytes = D * (int64_t)sizeof(XIn);
   const int64_t G = in_bytes / 16;
   const int out_unit = 16 / (int)sizeof(XIn) * (int)sizeof(XOut);
@@ -515,23 +550,24 @@ hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D,
     const int64_t blocks = tp.nseg() * nparts;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
     uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
-    segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK>
+    segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK, RT>
         <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, (int)G,
-                                                   nparts, out, omask, walk, tickets, tp.status);
+                                                   nparts, out, omask, walk, tickets, tp.status,
+                                                   nout);
     return hipGetLastError();
   }
   const int64_t nch_seg = (tp.T + kChunk - 1) / kChunk;
   const int64_t nchunks = tp.nseg() * nch_seg;
   const int64_t ncb = (D + kWave - 1) / kWave;
   const dim3 grid((unsigned)((nchunks + 3) / 4), (unsigned)ncb);
-  segsum_local_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK>
+  segsum_local_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK, RT>
       <<<grid, 256, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, nch_seg, nchunks, out, omask,
-                            tail, flag);
+                            tail, flag, nout);
   segsum_carry_kernel<Acc><<<dim3((unsigned)tp.nseg(), (unsigned)ncb), 1024, 0, s>>>(
       tail, flag, carry, nch_seg, D);
-  segsum_fixup_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK>
+  segsum_fixup_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK, RT>
       <<<grid, 256, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, nch_seg, nchunks, out, omask,
-                            carry);
+                            carry, nout);
   return hipGetLastError();
 }
 
@@ -590,7 +626,39 @@ hipError_t seg_sum_bwd_t(const U* sorted, const int32_t* spos, const void* grad_
       sorted, (const G*)gacc, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag, (Acc*)carry, walk, s);
 }
 
+template <int DT, typename U>
+hipError_t run_totals_t(const U* sorted, const void* rows, const Tape& tp, int64_t D, int64_t nout,
+                        void* out, void* tail, uint8_t* flag, void* carry, uint64_t* walk,
+                        hipStream_t s) {
+  using E = Elem<DT>;
+  using S = typename E::store_t;
+  using Acc = typename E::acc_t;
+  return run_segsum<U, S, S, Acc, E, E, false, false, true, false, false, true>(
+      sorted, (const S*)rows, tp, D, (S*)out, nullptr, (Acc*)tail, flag, (Acc*)carry, walk, s,
+      nout);
+}
+
 }  // namespace
+
+template <typename U>
+hipError_t run_totals(const U* sorted, const void* rows, int dtype, const Tape& tp, int64_t D,
+                      int64_t nout, void* out, void* tail, uint8_t* flag, void* carry,
+                      uint64_t* walk, hipStream_t s) {
+  switch (dtype) {
+    case kF32: return run_totals_t<kF32, U>(sorted, rows, tp, D, nout, out, tail, flag, carry, walk, s);
+    case kF64: return run_totals_t<kF64, U>(sorted, rows, tp, D, nout, out, tail, flag, carry, walk, s);
+    case kBF16: return run_totals_t<kBF16, U>(sorted, rows, tp, D, nout, out, tail, flag, carry, walk, s);
+    case kF16: return run_totals_t<kF16, U>(sorted, rows, tp, D, nout, out, tail, flag, carry, walk, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template hipError_t run_totals<uint32_t>(const uint32_t*, const void*, int, const Tape&, int64_t,
+                                         int64_t, void*, void*, uint8_t*, void*, uint64_t*,
+                                         hipStream_t);
+template hipError_t run_totals<uint64_t>(const uint64_t*, const void*, int, const Tape&, int64_t,
+                                         int64_t, void*, void*, uint8_t*, void*, uint64_t*,
+                                         hipStream_t);
 
 size_t seg_sum_chunks(const Tape& tp) {
   return (size_t)(tp.nseg() * ((tp.T + kChunk - 1) / kChunk));

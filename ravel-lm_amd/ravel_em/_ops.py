@@ -108,6 +108,8 @@ def latest_k_backward(src: Tensor, grad_values: Tensor, chain: bool) -> Tensor:
         nat.ptr(src), nat.ptr(grad_values), code, B, T, C, D, k, int(chain),
         nat.ptr(grad_payload), nat.ptr(ws), ws.numel(), nat.stream_of(grad_values),
     )
+    if not chain:  # the sorted form's workspace carries a status word
+        nat.after_call(ws)
     return grad_payload
 
 
