@@ -388,6 +388,18 @@ int seg_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   SumWs<U> w = take_sum<U>(bp, tp, D, dtype, direct, false);
   tp.status = w.sw.status;
   if (int rc = check_ws(bp, wsb)) return rc;
+  if (seg_sum_merged_applies(tp, D, dtype, payload, out_sum)) {
+    // short tapes: one block per segment, reads and writes merged in LDS
+    stage_begin(kStageSum, s);
+    AddrIn wd, rd;
+    hipError_t e = compact_addresses(wa, tp, w.sw.kb, &wd, s);
+    if (e == hipSuccess && ra) e = compact_addresses(*ra, tp, w.sw.ka, &rd, s);
+    if (e == hipSuccess)
+      e = seg_sum_merged(wd, ra ? &rd : nullptr, wmask, payload, dtype, tp, D, out_sum, out_mask, s);
+    stage_end(kStageSum, s);
+    if (e != hipSuccess) return hip_fail(e, "segmented sum");
+    return RAVEL_EM_OK;
+  }
   U* sorted = nullptr;
   stage_begin(kStageSort, s);
   hipError_t e = sort_call<U>(wa, wmask, tp, w.sw, &sorted, s, (uint32_t*)w.walk,

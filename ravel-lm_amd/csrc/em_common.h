@@ -284,6 +284,14 @@ template <typename U>
 hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& tp, int64_t D,
                    bool direct, void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag,
                    void* carry, uint64_t* walk, hipStream_t s);
+// The forward sum of a short tape in one launch (one block per segment, reads
+// and writes merged in LDS; no sort workspace): dense address inputs (ra null
+// = reads at the write addresses), rows of whole 16-byte units.
+bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
+                            const void* out);
+hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
+                          const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
+                          uint8_t* omask, hipStream_t s);
 size_t seg_sum_chunks(const Tape& tp);
 size_t acc_bytes(int dtype);
 size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype);

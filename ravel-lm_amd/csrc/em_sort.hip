@@ -18,6 +18,7 @@
 
 #include <type_traits>
 #include "em_common.h"
+#include "em_rank.h"
 
 namespace rem {
 
@@ -458,65 +459,6 @@ __global__ __launch_bounds__(1024) void scan_hist_kernel(const uint16_t* __restr
     if (g == 0) binbase[(seg * nh + p) * kRadix + d] = ex;
     __syncthreads();
   }
-}
-
-// Stable wave-striped ranking of one tile, shared by the pass-0 scatter and the
-// look-back sweeps.  On return: key/rank per item, wcnt[w][d] = exclusive
-// offsets of digit d over the block's waves, dstart[d] = exclusive offset of
-// digit d inside the tile; the thread with tid == d gets the tile count in *own.
-template <typename U, int ITEMS>
-__device__ __forceinline__ void load_tile(const U* __restrict__ src, int n, U* key) {
-  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int idx = w * kWave * ITEMS + i * kWave + lane;
-    key[i] = idx < n ? src[idx] : U(0);
-  }
-}
-
-// Keys must come from load_tile (wave-striped ownership).  NT threads (a
-// multiple of 256); the per-digit steps run on threads 0..255.
-template <typename U, int ITEMS, int NT = kSortThreads>
-__device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRadix],
-                                          uint32_t* dstart, uint32_t* scan_tmp, const U* key,
-                                          uint32_t* rank, uint32_t* own) {
-  constexpr int NW = NT / kWave;
-  static_assert(NT % kRadix == 0, "whole digit rows per thread group");
-  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
-#pragma unroll
-  for (int i = 0; i < NW * kRadix / NT; ++i) {
-    const int x = i * NT + tid;
-    wcnt[x / kRadix][x % kRadix] = 0;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int idx = w * kWave * ITEMS + i * kWave + lane;
-    const bool valid = idx < n;
-    const uint32_t d = (uint32_t)(key[i] >> shift) & (kRadix - 1);
-    const uint64_t peers = match_byte(d) & __ballot(valid);
-    uint32_t old = 0;
-    if (valid) old = wcnt[w][d];
-    const uint32_t below = count_below(peers);
-    __builtin_amdgcn_wave_barrier();
-    if (valid && below == 0)  // the lowest lane of the digit advances the counter
-      wcnt[w][d] = old + (uint32_t)__popcll(peers);
-    __builtin_amdgcn_wave_barrier();
-    rank[i] = old + below;
-  }
-  __syncthreads();
-  uint32_t tot = 0;
-  if (tid < kRadix) {
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      const uint32_t c = wcnt[i][tid];
-      wcnt[i][tid] = tot;
-      tot += c;
-    }
-  }
-  *own = tot;
-  const uint32_t ex = block_excl_scan<NT>(tot, scan_tmp, nullptr);
-  if (tid < kRadix) dstart[tid] = ex;
 }
 
 // Stage the ranked tile in LDS in local sorted order, then write each digit's

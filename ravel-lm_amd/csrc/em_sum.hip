@@ -28,6 +28,7 @@
 
 #include "em_common.h"
 #include "em_elem.h"
+#include "em_rank.h"
 
 namespace rem {
 
@@ -534,6 +535,306 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short tapes (T <= 4096): the whole forward sum of a segment in one block,
+// with reads and writes on one merged tape and no global sort.
+//   1. Item i < 2T is the read (i even) or the write (i odd) of time t = i/2,
+//      keyed a << (tbits + 1) | i, with a the read or write address (a masked
+//      write at the sentinel A).  The items are already in (time, kind)
+//      order, so stable LSD passes over the address bits alone (in LDS) leave
+//      each address's run in time order with a read before the write of its
+//      own time: a read sees exactly the writes of its stream before it.
+//   2. The last read of every run (an LDS table when A <= kMergedLr): a write
+//      with no read after it in its run feeds no output and is not loaded.
+//   3. The segmented-sum walk over the merged run (walkers of G lanes, tails,
+//      a fold over the walkers, then the walk): writes add their payload row,
+//      each read stores the running sum and the mask (some write before it).
+// So the prefix rows are never stored and re-read, and reads need no search.
+constexpr int kMergedThreads = 512;  // two blocks per CU (LDS and registers)
+constexpr int kMergedItems = 8192;  // 2T
+constexpr int kMergedLr = 4096;     // addresses of the last-read table
+// bytes: sort counters + last-read table, then the walker tails (32 KiB at
+// most: 1024 x 16 bytes of payload as accumulators) and the fold's group sums
+// (at most kMergedThreads accumulators)
+constexpr int kMergedUnion = 40960;
+
+// An address input of any dense kind (one load per item, so a runtime switch).
+struct AnyDense {
+  const void* p;
+  int kind;
+  int64_t T, C;
+  __device__ __forceinline__ int64_t operator()(int64_t b, int64_t t, int64_t c) const {
+    const int64_t i = (b * T + t) * C + c;
+    switch (kind) {
+      case kI32: return (int64_t)((const int32_t*)p)[i];
+      case kI64: return ((const int64_t*)p)[i];
+      case kU16: return (int64_t)((const uint16_t*)p)[i];
+      default: return (int64_t)((const uint32_t*)p)[i];
+    }
+  }
+};
+
+template <int ITEMS, typename XIn, typename Acc, typename LoadF, typename StoreF>
+__global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void segsum_merged_kernel(
+    const AnyDense waddr, const AnyDense raddr, const uint8_t* __restrict__ wmask, int64_t T,
+    int64_t C, int64_t A, int tbits, int npass, int trunc32, int G, int64_t nseg,
+    const XIn* __restrict__ payload, XIn* __restrict__ out, uint8_t* __restrict__ omask,
+    uint32_t* __restrict__ status) {
+  constexpr int NT = kMergedThreads;
+  constexpr int NWV = NT / kWave;
+  constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
+  using OutV = typename Unit<CPU * (int)sizeof(XIn)>::T;
+  __shared__ __align__(16) uint32_t keys[kMergedItems];
+  __shared__ __align__(16) unsigned char un[kMergedUnion];
+  __shared__ uint32_t dstart[kRankRadix];
+  __shared__ uint32_t scan_tmp[NWV + 1];
+  __shared__ uint32_t needw[kMergedItems / 32];  // write i is loaded
+  __shared__ uint8_t hs[NT], hw[NT], hwin[NT];   // per walker
+  static_assert(NWV * kRankRadix * sizeof(uint32_t) + kMergedLr * sizeof(uint32_t) <= kMergedUnion,
+                "counters and last-read table share the union");
+  const int tid = threadIdx.x, wv = tid / kWave, lane = tid % kWave;
+  if (blockIdx.x == 0 && tid == 0) *status = 0;  // the call's only kernel: no waits
+  const int64_t seg = xcd_block(blockIdx.x, gridDim.x);
+  if (seg >= nseg) return;  // uniform per block
+  const int64_t b = seg / C, c = seg - (seg / C) * C;
+  const int n2 = (int)(2 * T);
+  const int tb1 = tbits + 1;
+  // 1. merged keys (straight to LDS), then the address passes.  A thread's
+  // address (and mask) loads are all issued before any is used.
+  constexpr int KB = ITEMS;  // items per thread (n2 <= NT * ITEMS)
+  for (int base = 0; base < n2; base += NT * KB) {
+    int64_t av[KB];
+    uint8_t mv[KB];
+#pragma unroll
+    for (int m = 0; m < KB; ++m) {
+      const int i = base + m * NT + tid;
+      const int64_t t = (i < n2 ? i : 0) >> 1;
+      const bool wr = i & 1;
+      av[m] = wr ? waddr(b, t, c) : raddr(b, t, c);
+      mv[m] = (wr && wmask) ? wmask[b * T + t] : 1;
+    }
+#pragma unroll
+    for (int m = 0; m < KB; ++m) {
+      const int i = base + m * NT + tid;
+      if (i < n2) {
+        int64_t a = reduce_addr(av[m], A, kWrap, trunc32 != 0);
+        if (!mv[m]) a = A;
+        keys[i] = ((uint32_t)a << tb1) | (uint32_t)i;
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t (*wcnt)[kRankRadix] = (uint32_t (*)[kRankRadix])un;
+  uint32_t key[ITEMS];
+  if (npass > 0) load_tile<uint32_t, ITEMS>(keys, n2, key);
+  for (int p = 0; p < npass; ++p) {
+    const int shift = tb1 + 8 * p;
+    uint32_t rank[ITEMS];
+    uint32_t own;
+    rank_tile<uint32_t, ITEMS, NT>(n2, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+    __syncthreads();  // dstart of every digit; every thread's keys are in registers
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int i = wv * kWave * ITEMS + it * kWave + lane;
+      if (i < n2) {
+        const uint32_t d = (key[it] >> shift) & (kRankRadix - 1);
+        keys[dstart[d] + wcnt[wv][d] + rank[it]] = key[it];
+      }
+    }
+    __syncthreads();
+    if (p + 1 < npass) load_tile<uint32_t, ITEMS>(keys, n2, key);
+  }
+  __syncthreads();
+  // 2. writes that some later read of their run needs
+  const bool table = A <= kMergedLr;
+  uint32_t* lr = (uint32_t*)(un + NWV * kRankRadix * sizeof(uint32_t));  // last read + 1
+  if (table) {
+    for (int i = tid; i < A; i += NT) lr[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n2; i += NT) {
+      const uint32_t k = keys[i];
+      if (!(k & 1u)) atomicMax(&lr[k >> tb1], (uint32_t)(i + 1));
+    }
+    __syncthreads();
+  }
+  for (int i0 = wv * kWave; i0 < n2; i0 += NT) {
+    const int i = i0 + lane;
+    bool need = false;
+    if (i < n2) {
+      const uint32_t k = keys[i];
+      const uint32_t a = k >> tb1;
+      need = (k & 1u) && a < (uint32_t)A && (!table || (uint32_t)(i + 1) < lr[a]);
+    }
+    const uint64_t m = __ballot(need);
+    if (lane == 0) {
+      needw[i0 >> 5] = (uint32_t)m;
+      if (i0 + 32 < kMergedItems) needw[(i0 >> 5) + 1] = (uint32_t)(m >> 32);
+    }
+  }
+  __syncthreads();
+  // 3. the walk: walker w owns items [rs, re)
+  const int NW = NT / G;
+  const int w = tid / G, v = tid - (tid / G) * G;
+  const int len = (n2 + NW - 1) / NW;
+  const int rs = w * len < n2 ? w * len : n2;
+  const int re = (rs + len) < n2 ? (rs + len) : n2;
+  const uint32_t tmask1 = (1u << tb1) - 1u;
+  auto start = [&](int i) -> bool { return i == 0 || (keys[i] >> tb1) != (keys[i - 1] >> tb1); };
+  auto needed = [&](int i) -> bool { return (needw[i >> 5] >> (i & 31)) & 1u; };
+  const int32_t rbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+  auto rec = [&](int i) -> int32_t { return rbase + (int32_t)((keys[i] & tmask1) >> 1) * Ci; };
+  const u32x4* inv = (const u32x4*)payload;
+  // tail: from the range's last run start (or its start) to its end
+  int last = -1;
+  for (int i = rs + v; i < re; i += G)
+    if (start(i)) last = i;
+  for (int o = 1; o < G; o <<= 1) {
+    const int other = __shfl_xor(last, o, kWave);
+    last = other > last ? other : last;
+  }
+  Acc acc[CPU];
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+  bool hwt = false;
+  for (int i0 = (last >= 0 ? last : rs); i0 < re; i0 += kWalkBatch) {
+    u32x4 x[kWalkBatch];
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
+      x[m] = needed(i) ? inv[(int64_t)rec(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m)
+      if (i0 + m < re) {
+        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
+        hwt = hwt || needed(i0 + m);
+      }
+  }
+  const int ncol = G * CPU;  // == D
+  Acc* tl = (Acc*)un;        // [walker][column]; the counters and table are dead
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) tl[w * ncol + v * CPU + j] = acc[j];
+  if (v == 0) {
+    hs[w] = last >= 0 ? 1 : 0;
+    hw[w] = hwt ? 1 : 0;
+  }
+  __syncthreads();
+  // fold: the carry into each walker, a segmented scan over the walkers (a
+  // run start resets) of the column sums and of the has-a-write flags.
+  // Thread (g, col) folds walkers [g*chunk, (g+1)*chunk) of its column, then
+  // takes the aggregates of the groups before g, then rewrites its chunk with
+  // the carries.  NG <= 64 groups keep the serial steps short.
+  {
+    const int NG = (NT / ncol) < 64 ? (NT / ncol) : 64;  // >= 1 (ncol <= 512)
+    const int chunk = NW / NG;
+    Acc* gsum = (Acc*)(un + (size_t)NW * ncol * sizeof(Acc));  // [NG][ncol] after tl
+    uint8_t* gflag = hwin;  // [NG] group has a run start; hwin is rewritten below
+    uint8_t* ghw = hwin + 64;  // [NG] group's has-a-write after its last start
+    const int col = tid % ncol, g = tid / ncol;
+    if (g < NG) {
+      Acc x = Acc(0);
+      bool f = false, h = false;
+      for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
+        const Acc t = tl[k * ncol + col];
+        x = hs[k] ? t : x + t;
+        h = hs[k] ? (hw[k] != 0) : (h || hw[k] != 0);
+        f = f || hs[k];
+      }
+      gsum[g * ncol + col] = x;
+      if (col == 0) {
+        gflag[g] = f ? 1 : 0;
+        ghw[g] = h ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    Acc cin = Acc(0);
+    bool hin = false;
+    if (g < NG) {
+      for (int q = 0; q < g; ++q) {
+        const Acc t = gsum[q * ncol + col];
+        cin = gflag[q] ? t : cin + t;
+        hin = gflag[q] ? (ghw[q] != 0) : (hin || ghw[q] != 0);
+      }
+    }
+    __syncthreads();  // the group arrays (in hwin) are read; hwin is written next
+    if (g < NG) {
+      for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
+        const Acc t = tl[k * ncol + col];
+        tl[k * ncol + col] = cin;
+        cin = hs[k] ? t : cin + t;
+        if (col == 0) hwin[k] = hin ? 1 : 0;
+        hin = hs[k] ? (hw[k] != 0) : (hin || hw[k] != 0);
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
+  bool hasw = hwin[w] != 0;
+  OutV* ou = (OutV*)out + v;  // unit v of row r is ou[r * G]
+  for (int i0 = rs; i0 < re; i0 += kWalkBatch) {
+    u32x4 x[kWalkBatch];
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
+      x[m] = needed(i) ? __builtin_nontemporal_load(&inv[(int64_t)rec(i) * G + v])
+                       : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int m = 0; m < kWalkBatch; ++m) {
+      const int i = i0 + m;
+      if (i < re) {
+        if (start(i)) {
+#pragma unroll
+          for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+          hasw = false;
+        }
+        if (keys[i] & 1u) {  // a write
+          if (needed(i)) {
+            add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
+            hasw = true;
+          }
+        } else {  // a read: its sum and mask
+          const int32_t r = rec(i);
+          __builtin_nontemporal_store(pack_unit<XIn, StoreF, Acc, CPU>(acc), &ou[(int64_t)r * G]);
+          if (v == 0) omask[r] = hasw ? 1 : 0;
+        }
+      }
+    }
+  }
+}
+
+bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, const void* out) {
+  const int64_t G = row_bytes / 16;
+  return tp.T >= 1 && 2 * tp.T <= kMergedItems && tp.abits + tp.tbits + 1 <= 32 &&
+         row_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
+         (((uintptr_t)payload | (uintptr_t)out) & 15) == 0 && tp.nseg() <= INT32_MAX;
+}
+
+template <int DT>
+hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn& ra, const uint8_t* wmask,
+                            const void* payload, const Tape& tp, int64_t D, void* out,
+                            uint8_t* omask, hipStream_t s) {
+  using E = Elem<DT>;
+  using S = typename E::store_t;
+  using Acc = typename E::acc_t;
+  const AnyDense w{wa.dense, wa.kind, tp.T, tp.C}, r{ra.dense, ra.kind, tp.T, tp.C};
+  const int64_t G = D * (int64_t)sizeof(S) / 16;
+  const int npass = (tp.abits + 7) / 8;
+  const unsigned grid = xcd_grid(tp.nseg(), 1, (int64_t)1 << 31);
+#define REM_MG(IT)                                                                           \
+  segsum_merged_kernel<IT, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                     \
+      w, r, wmask, tp.T, tp.C, tp.A, tp.tbits, npass, tp.trunc32 ? 1 : 0, (int)G, tp.nseg(), \
+      (const S*)payload, (S*)out, omask, tp.status)
+  if (2 * tp.T <= 4 * kMergedThreads)
+    REM_MG(4);
+  else
+    REM_MG(16);
+#undef REM_MG
+  return hipGetLastError();
+}
+
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
           bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT = false>
 hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D, XOut* out,
@@ -680,6 +981,25 @@ hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& 
     case kF64: return seg_sum_t<kF64, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
     case kBF16: return seg_sum_t<kBF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
     case kF16: return seg_sum_t<kF16, U>(sorted, payload, tp, D, direct, out_or_S, omask, tail, flag, carry, walk, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
+                            const void* out) {
+  return merged_applies(tp, D * dtype_size(dtype), payload, out);
+}
+
+hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
+                          const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
+                          uint8_t* omask, hipStream_t s) {
+  if (!tp.status) return hipErrorInvalidValue;
+  const AddrIn& r = ra ? *ra : wa;
+  switch (dtype) {
+    case kF32: return seg_sum_merged_t<kF32>(wa, r, wmask, payload, tp, D, out, omask, s);
+    case kF64: return seg_sum_merged_t<kF64>(wa, r, wmask, payload, tp, D, out, omask, s);
+    case kBF16: return seg_sum_merged_t<kBF16>(wa, r, wmask, payload, tp, D, out, omask, s);
+    case kF16: return seg_sum_merged_t<kF16>(wa, r, wmask, payload, tp, D, out, omask, s);
     default: return hipErrorInvalidValue;
   }
 }
