@@ -30,6 +30,8 @@
 #include "em_elem.h"
 #include "em_rank.h"
 
+#include <type_traits>
+
 namespace rem {
 
 namespace {
@@ -557,6 +559,12 @@ constexpr int kMergedLr = 4096;     // addresses of the last-read table
 // most: 1024 x 16 bytes of payload as accumulators) and the fold's group sums
 // (at most kMergedThreads accumulators)
 constexpr int kMergedUnion = 40960;
+// merged-tape code words (the time in bits 0..23)
+constexpr uint32_t kCodeStart = 1u << 29, kCodeNoStore = 1u << 30, kCodeNoLoad = 1u << 31;
+// gfx9 buffer descriptor word 3 (raw 32-bit access), and the nontemporal
+// cache-policy bit of buffer loads and stores
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kBufNontemporal = 2;
 
 // An address input of any dense kind (one load per item, so a runtime switch).
 struct AnyDense {
@@ -588,7 +596,6 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   __shared__ __align__(16) unsigned char un[kMergedUnion];
   __shared__ uint32_t dstart[kRankRadix];
   __shared__ uint32_t scan_tmp[NWV + 1];
-  __shared__ uint32_t needw[kMergedItems / 32];  // write i is loaded
   __shared__ uint8_t hs[NT], hw[NT], hwin[NT];   // per walker
   static_assert(NWV * kRankRadix * sizeof(uint32_t) + kMergedLr * sizeof(uint32_t) <= kMergedUnion,
                 "counters and last-read table share the union");
@@ -645,7 +652,10 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     if (p + 1 < npass) load_tile<uint32_t, ITEMS>(keys, n2, key);
   }
   __syncthreads();
-  // 2. writes that some later read of their run needs
+  // 2. one code word per item, over its key: bits 0..23 the time, bit 29 a
+  // run start, bit 30 no store (a write), bit 31 no load (a read, or a write
+  // no later read of its run needs).  Items [n2, n2r) pad the walkers'
+  // ranges to whole batches as writes that are not loaded.
   const bool table = A <= kMergedLr;
   uint32_t* lr = (uint32_t*)(un + NWV * kRankRadix * sizeof(uint32_t));  // last read + 1
   if (table) {
@@ -657,59 +667,106 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
     __syncthreads();
   }
-  for (int i0 = wv * kWave; i0 < n2; i0 += NT) {
-    const int i = i0 + lane;
-    bool need = false;
-    if (i < n2) {
-      const uint32_t k = keys[i];
-      const uint32_t a = k >> tb1;
-      need = (k & 1u) && a < (uint32_t)A && (!table || (uint32_t)(i + 1) < lr[a]);
+  const int n2r = (n2 + kWalkBatch - 1) & ~(kWalkBatch - 1);  // <= kMergedItems
+  const uint32_t tmask1 = (1u << tb1) - 1u;
+  {
+    uint32_t cw[ITEMS];
+#pragma unroll
+    for (int m = 0; m < ITEMS; ++m) {
+      const int i = m * NT + tid;
+      cw[m] = kCodeNoLoad | kCodeNoStore;
+      if (i < n2) {
+        const uint32_t k = keys[i];
+        const uint32_t a = k >> tb1;
+        const bool st = i == 0 || (keys[i - 1] >> tb1) != a;
+        const bool wr = k & 1u;
+        const bool need = wr && a < (uint32_t)A && (!table || (uint32_t)(i + 1) < lr[a]);
+        cw[m] = (st ? kCodeStart : 0u) | (wr ? kCodeNoStore : 0u) | (need ? 0u : kCodeNoLoad) |
+                ((k & tmask1) >> 1);
+      }
     }
-    const uint64_t m = __ballot(need);
-    if (lane == 0) {
-      needw[i0 >> 5] = (uint32_t)m;
-      if (i0 + 32 < kMergedItems) needw[(i0 >> 5) + 1] = (uint32_t)(m >> 32);
+    __syncthreads();  // every key is read
+#pragma unroll
+    for (int m = 0; m < ITEMS; ++m) {
+      const int i = m * NT + tid;
+      if (i < n2r) keys[i] = cw[m];
     }
   }
   __syncthreads();
-  // 3. the walk: walker w owns items [rs, re)
+  // 3. the walk: walker w owns items [rs, re), whole batches
   const int NW = NT / G;
   const int w = tid / G, v = tid - (tid / G) * G;
-  const int len = (n2 + NW - 1) / NW;
-  const int rs = w * len < n2 ? w * len : n2;
-  const int re = (rs + len) < n2 ? (rs + len) : n2;
-  const uint32_t tmask1 = (1u << tb1) - 1u;
-  auto start = [&](int i) -> bool { return i == 0 || (keys[i] >> tb1) != (keys[i - 1] >> tb1); };
-  auto needed = [&](int i) -> bool { return (needw[i >> 5] >> (i & 31)) & 1u; };
-  const int32_t rbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
-  auto rec = [&](int i) -> int32_t { return rbase + (int32_t)((keys[i] & tmask1) >> 1) * Ci; };
-  const u32x4* inv = (const u32x4*)payload;
-  // tail: from the range's last run start (or its start) to its end
+  const int len = (((n2r + NW - 1) / NW) + kWalkBatch - 1) & ~(kWalkBatch - 1);
+  const int rs = w * len < n2r ? w * len : n2r;
+  const int re = (rs + len) < n2r ? (rs + len) : n2r;
+  // The segment's rows through buffer descriptors: row t's unit v is at byte
+  // t * tstride + 16 v of the segment's base in the payload and the output
+  // (one layout), its mask byte at t * C.  A set code bit 30 or 31 (>= 2^30,
+  // beyond every range) turns a load into zeros and a store into nothing, so
+  // the walk has no branches.
+  const uint32_t tstride = (uint32_t)(C * G * 16);
+  const int64_t rbase = b * T * C + c;
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const unsigned char*)payload + rbase * G * 16), 0, (int)(T * tstride), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((unsigned char*)out + rbase * G * 16), 0, (int)(T * tstride), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t mrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(omask + rbase), 0, (int)(T * C), kRsrcWord3);
+  const uint32_t v16 = (uint32_t)v * 16u, Cu = (uint32_t)C;
+  const uint32_t mlane = v == 0 ? 0u : kCodeNoStore;  // one mask store per walker
+  Acc acc[CPU];
+  bool hasw = false;
+  // Items [i0, i1) of the range: a run start resets the sum and the has-a-
+  // write flag, a loaded write adds its row, a read (STORE) stores the sum and
+  // the flag.  The final walk streams its rows past the caches.
+  auto walk = [&](int i0, int i1, auto store_tag) {
+    constexpr bool STORE = decltype(store_tag)::value;
+    constexpr int aux = STORE ? kBufNontemporal : 0;
+    for (; i0 < i1; i0 += kWalkBatch) {
+      uint32_t cw[kWalkBatch];
+#pragma unroll
+      for (int q = 0; q < kWalkBatch / 4; ++q) {
+        const u32x4 c4 = *(const u32x4*)&keys[i0 + 4 * q];
+        cw[4 * q] = c4.x, cw[4 * q + 1] = c4.y, cw[4 * q + 2] = c4.z, cw[4 * q + 3] = c4.w;
+      }
+      u32x4 x[kWalkBatch];
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m)
+        x[m] = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad), 0, aux);
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m) {
+        const uint32_t k = cw[m];
+        const bool st = k & kCodeStart;
+#pragma unroll
+        for (int j = 0; j < CPU; ++j) acc[j] = st ? Acc(0) : acc[j];
+        hasw = hasw && !st;
+        if (STORE) {
+          const uint32_t ns = k & kCodeNoStore;
+          __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XIn, StoreF, Acc, CPU>(acc), ors,
+                                                 (__umul24(k, tstride) + v16) | ns, 0, aux);
+          __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(hasw ? 1 : 0), mrs,
+                                               (__umul24(k, Cu) | mlane) | ns, 0, 0);
+        }
+        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
+        hasw = hasw || !(k & kCodeNoLoad);
+      }
+    }
+  };
+  // tail: from the range's last run start (or its start) to its end; the
+  // batch holding that start may begin before it, whose items the start's
+  // reset discards.
   int last = -1;
   for (int i = rs + v; i < re; i += G)
-    if (start(i)) last = i;
+    if (keys[i] & kCodeStart) last = i;
   for (int o = 1; o < G; o <<= 1) {
     const int other = __shfl_xor(last, o, kWave);
     last = other > last ? other : last;
   }
-  Acc acc[CPU];
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
-  bool hwt = false;
-  for (int i0 = (last >= 0 ? last : rs); i0 < re; i0 += kWalkBatch) {
-    u32x4 x[kWalkBatch];
-#pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m) {
-      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = needed(i) ? inv[(int64_t)rec(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m)
-      if (i0 + m < re) {
-        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
-        hwt = hwt || needed(i0 + m);
-      }
-  }
+  walk(last >= 0 ? (last & ~(kWalkBatch - 1)) : rs, re, std::false_type{});
+  const bool hwt = hasw;
   const int ncol = G * CPU;  // == D
   Acc* tl = (Acc*)un;        // [walker][column]; the counters and table are dead
   __syncthreads();
@@ -771,45 +828,16 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
-  bool hasw = hwin[w] != 0;
-  OutV* ou = (OutV*)out + v;  // unit v of row r is ou[r * G]
-  for (int i0 = rs; i0 < re; i0 += kWalkBatch) {
-    u32x4 x[kWalkBatch];
-#pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m) {
-      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = needed(i) ? __builtin_nontemporal_load(&inv[(int64_t)rec(i) * G + v])
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m) {
-      const int i = i0 + m;
-      if (i < re) {
-        if (start(i)) {
-#pragma unroll
-          for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
-          hasw = false;
-        }
-        if (keys[i] & 1u) {  // a write
-          if (needed(i)) {
-            add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
-            hasw = true;
-          }
-        } else {  // a read: its sum and mask
-          const int32_t r = rec(i);
-          __builtin_nontemporal_store(pack_unit<XIn, StoreF, Acc, CPU>(acc), &ou[(int64_t)r * G]);
-          if (v == 0) omask[r] = hasw ? 1 : 0;
-        }
-      }
-    }
-  }
+  hasw = hwin[w] != 0;
+  walk(rs, re, std::true_type{});
 }
 
 bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, const void* out) {
   const int64_t G = row_bytes / 16;
   return tp.T >= 1 && 2 * tp.T <= kMergedItems && tp.abits + tp.tbits + 1 <= 32 &&
          row_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
-         (((uintptr_t)payload | (uintptr_t)out) & 15) == 0 && tp.nseg() <= INT32_MAX;
+         (((uintptr_t)payload | (uintptr_t)out) & 15) == 0 && tp.nseg() <= INT32_MAX &&
+         tp.C * row_bytes < ((int64_t)1 << 24) && tp.T * tp.C * row_bytes <= ((int64_t)1 << 30);
 }
 
 template <int DT>

@@ -43,6 +43,7 @@ TINY = {torch.float32: 2.0 ** -149, torch.float64: 2.0 ** -1074, torch.bfloat16:
 def sum_depth(T: int, D: int, dtype: torch.dtype, walker: bool = True) -> int:
     """Longest addition chain of one term in the GPU summation (em_sum.hip).
 
+    Merged kernel (2T <= 8192, the same rows): see the comment in the body.
     Walker kernel (rows of 1..64 whole 16-byte units, 16-byte aligned): a part
     of 1024 positions is split over NW = 256 / G walkers of L = 1024 / NW
     positions; a term is added along its walker's tail (<= L), the part's fold
@@ -54,7 +55,17 @@ def sum_depth(T: int, D: int, dtype: torch.dtype, walker: bool = True) -> int:
     G = row // 16
     if walker and row % 16 == 0 and 1 <= G <= 64 and G & (G - 1) == 0:
         nw = 256 // G
-        return 2 * (1024 // nw) + 2 * nw + math.ceil(T / 1024)
+        depth = 2 * (1024 // nw) + 2 * nw + math.ceil(T / 1024)
+        if 2 * T <= 8192:
+            # short tapes may take the one-block merged kernel: 2T items over
+            # NW = 512 / G walkers of L items (a multiple of 16), the walkers'
+            # tails folded in NG groups of NW / NG (NG = min(64, 512 / D))
+            nw = 512 // G
+            n2r = -(-2 * T // 16) * 16
+            L = -(-(-(-n2r // nw)) // 16) * 16
+            ng = min(64, 512 // D)
+            depth = max(depth, 2 * L + 2 * (nw // ng) + ng)
+        return depth
     nch = math.ceil(T / 64)
     return 64 + 2 * math.ceil(nch / 16) + 16 + 64
 
