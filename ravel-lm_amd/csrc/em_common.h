@@ -81,6 +81,16 @@ struct AddrIn {
 constexpr uint32_t kStatusSortWait = 1u;  // a sort pass's tile look-back
 constexpr uint32_t kStatusSumWait = 2u;   // the segmented sum's part look-back
 constexpr size_t kStatusBytes = 256;
+// words 2-3 of the status area: the merged sum kernel's start gate (a
+// launch sequence number and a count; a scheduling hint, never an error)
+constexpr int kStatusGateWord = 2;
+
+// Compute units and wall-clock rate (kHz) of a device, queried once.
+struct DeviceShape {
+  int cus = 256;
+  int wall_khz = 100000;
+};
+const DeviceShape& device_shape(int dev);
 
 int bit_width_u64(uint64_t x);
 Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);
@@ -284,9 +294,9 @@ template <typename U>
 hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& tp, int64_t D,
                    bool direct, void* out_or_S, uint8_t* omask, void* tail, uint8_t* flag,
                    void* carry, uint64_t* walk, hipStream_t s);
-// The forward sum of a short tape in one launch (one block per segment, reads
-// and writes merged in LDS; no sort workspace): dense address inputs (ra null
-// = reads at the write addresses), rows of whole 16-byte units.
+// The forward sum of a short tape in one launch (one block per segment,
+// reads and writes merged in LDS; no sort workspace): dense address inputs
+// (ra null = reads at the write addresses), rows of whole 16-byte units.
 bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
                             const void* out);
 hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,

@@ -25,10 +25,19 @@ __device__ __forceinline__ void load_tile(const U* __restrict__ src, int n, U* k
 
 // Keys must come from load_tile (wave-striped ownership).  NT threads (a
 // multiple of 256); the per-digit steps run on threads 0..255.
-template <typename U, int ITEMS, int NT = 256>
+//
+// The lanes of a wave holding the same digit ("peers") come from one of two
+// forms: eight ballots (one per digit bit), or, with PEER_TABLE and a table mt
+// ([waves][256] 64-bit lane masks, all zero, left zero on return), an LDS OR
+// of each lane's bit into its digit's entry, read back, then cleared by the
+// digit's lowest lane: three LDS operations in place of some 40 VALU.  One
+// wave's LDS operations run in issue order, so the read sees every lane's OR
+// and the clear follows every read.
+template <typename U, int ITEMS, int NT = 256, bool PEER_TABLE = false>
 __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRankRadix],
                                           uint32_t* dstart, uint32_t* scan_tmp, const U* key,
-                                          uint32_t* rank, uint32_t* own) {
+                                          uint32_t* rank, uint32_t* own,
+                                          uint64_t (*mt)[kRankRadix] = nullptr) {
   constexpr int NW = NT / kWave;
   static_assert(NT % kRankRadix == 0, "whole digit rows per thread group");
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
@@ -38,18 +47,31 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
     wcnt[x / kRankRadix][x % kRankRadix] = 0;
   }
   __syncthreads();
+  const uint64_t lane_bit = 1ull << lane;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int idx = w * kWave * ITEMS + i * kWave + lane;
     const bool valid = idx < n;
     const uint32_t d = (uint32_t)(key[i] >> shift) & (kRankRadix - 1);
-    const uint64_t peers = match_byte(d) & __ballot(valid);
+    uint64_t peers = 0;
     uint32_t old = 0;
-    if (valid) old = wcnt[w][d];
+    if (PEER_TABLE) {
+      if (valid) atomicOr((unsigned long long*)&mt[w][d], (unsigned long long)lane_bit);
+      __builtin_amdgcn_wave_barrier();
+      if (valid) {
+        peers = mt[w][d];
+        old = wcnt[w][d];
+      }
+    } else {
+      peers = match_byte(d) & __ballot(valid);
+      if (valid) old = wcnt[w][d];
+    }
     const uint32_t below = count_below(peers);
     __builtin_amdgcn_wave_barrier();
-    if (valid && below == 0)  // the lowest lane of the digit advances the counter
+    if (valid && below == 0) {  // the lowest lane of the digit advances the counter
       wcnt[w][d] = old + (uint32_t)__popcll(peers);
+      if (PEER_TABLE) mt[w][d] = 0;
+    }
     __builtin_amdgcn_wave_barrier();
     rank[i] = old + below;
   }

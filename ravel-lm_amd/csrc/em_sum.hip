@@ -30,6 +30,7 @@
 #include "em_elem.h"
 #include "em_rank.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace rem {
@@ -561,37 +562,98 @@ constexpr int kMergedLr = 4096;     // addresses of the last-read table
 constexpr int kMergedUnion = 40960;
 // merged-tape code words (the time in bits 0..23)
 constexpr uint32_t kCodeStart = 1u << 29, kCodeNoStore = 1u << 30, kCodeNoLoad = 1u << 31;
+constexpr uint32_t kCodeTime = (1u << 24) - 1u;
+// the reads' mask bytes in the union during the final walk: T entries and a
+// spare byte, clear of the walker tails and the fold's group sums
+constexpr int kMergedMaskOff = 32768;
+// the walkers' first run starts (at most kMergedThreads ints), between the two
+constexpr int kMergedStartOff = 20480;
+static_assert(kMergedMaskOff + kMergedItems / 2 + 1 <= kMergedUnion, "mask bytes fit");
 // gfx9 buffer descriptor word 3 (raw 32-bit access), and the nontemporal
 // cache-policy bit of buffer loads and stores
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr int kBufNontemporal = 2;
 
-// An address input of any dense kind (one load per item, so a runtime switch).
-struct AnyDense {
-  const void* p;
-  int kind;
-  int64_t T, C;
-  __device__ __forceinline__ int64_t operator()(int64_t b, int64_t t, int64_t c) const {
-    const int64_t i = (b * T + t) * C + c;
-    switch (kind) {
-      case kI32: return (int64_t)((const int32_t*)p)[i];
-      case kI64: return ((const int64_t*)p)[i];
-      case kU16: return (int64_t)((const uint16_t*)p)[i];
-      default: return (int64_t)((const uint32_t*)p)[i];
-    }
+// Start gate of the merged kernel.  With every block resident at once, all
+// blocks would sort (LDS-bound) together and then walk (HBM-bound) together.
+// Blocks [gate_lo, gate_hi) (the second block of each CU) instead wait until
+// gate_target of the blocks below gate_lo have finished their sort, so one
+// block per CU sorts while the other walks.  The gate word holds the low 16
+// bits of the launch's sequence number (high half, stored by block 0 as the
+// kernel starts) and the count of finished sorts (low half, one atomic add
+// each).  The wait is a scheduling hint only: it ends after gate_ticks of the
+// wall clock whatever the word says, and nothing the kernel computes depends
+// on it.
+__device__ __forceinline__ void gate_wait(const uint32_t* gate, uint32_t tag, uint32_t target,
+                                          uint32_t ticks) {
+  const uint64_t t0 = wall_clock64();
+  for (;;) {
+    const uint32_t v = __hip_atomic_load(gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((v >> 16) == tag && (v & 0xffffu) >= target) return;
+    if (wall_clock64() - t0 >= ticks) return;
+    __builtin_amdgcn_s_sleep(4);
   }
+}
+
+// One segment's column of a dense [B, T, C] address tensor (2, 4 or 8-byte
+// elements; time t at byte t * stride of base) through a buffer descriptor:
+// each element is read as the two dwords from the aligned dword holding it,
+// so the loads have no branches on the element kind and all issue before any
+// is used.  The range check reads zeros past the tensor's last dword and for
+// an offset of 2^31.
+struct AddrCol {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t stride;
+  int esize;
+  bool sign;  // int32 / int64 elements
 };
+
+__device__ __forceinline__ AddrCol addr_col(const void* p, int kind, int64_t b, int64_t c,
+                                            int64_t T, int64_t C) {
+  AddrCol col;
+  col.esize = kind == kI64 ? 8 : (kind == kU16 ? 2 : 4);
+  col.sign = kind == kI64 || kind == kI32;
+  col.stride = (uint32_t)(C * col.esize);
+  const unsigned char* base = (const unsigned char*)p + (b * T * C + c) * col.esize;
+  // the dword holding a 2-byte element may reach 2 bytes past the last one
+  const int64_t bytes = ((T - 1) * C * col.esize + col.esize + 3) & ~(int64_t)3;
+  col.rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, kRsrcWord3);
+  return col;
+}
+
+__device__ __forceinline__ void addr_col_load(const AddrCol& col, uint32_t t, bool ok,
+                                              uint32_t* lo, uint32_t* hi) {
+  const uint32_t off = t * col.stride;
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(col.rs, (off & ~3u) | (ok ? 0u : 0x80000000u),
+                                                       0, 0);
+  *lo = v.x;
+  *hi = v.y;
+}
+
+__device__ __forceinline__ int64_t addr_col_value(const AddrCol& col, uint32_t t, uint32_t lo,
+                                                  uint32_t hi) {
+  if (col.esize == 2) return (int64_t)((lo >> (((t * col.stride) & 2u) * 8u)) & 0xffffu);
+  if (col.esize == 4) return col.sign ? (int64_t)(int32_t)lo : (int64_t)lo;
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 template <int ITEMS, typename XIn, typename Acc, typename LoadF, typename StoreF>
 __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void segsum_merged_kernel(
-    const AnyDense waddr, const AnyDense raddr, const uint8_t* __restrict__ wmask, int64_t T,
-    int64_t C, int64_t A, int tbits, int npass, int trunc32, int G, int64_t nseg,
-    const XIn* __restrict__ payload, XIn* __restrict__ out, uint8_t* __restrict__ omask,
-    uint32_t* __restrict__ status) {
+    const void* __restrict__ waddr, int wkind, const void* __restrict__ raddr, int rkind,
+    const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int trunc32, int tbits,
+    int npass, int G, int64_t nseg, const XIn* __restrict__ payload,
+    XIn* __restrict__ out, uint8_t* __restrict__ omask, uint32_t* __restrict__ status,
+    uint32_t* __restrict__ gate, uint32_t tag, uint32_t gate_lo, uint32_t gate_hi,
+    uint32_t gate_target, uint32_t gate_ticks) {
   constexpr int NT = kMergedThreads;
   constexpr int NWV = NT / kWave;
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
   using OutV = typename Unit<CPU * (int)sizeof(XIn)>::T;
+  static_assert(NT * CPU * sizeof(Acc) + NT * sizeof(Acc) <= kMergedMaskOff,
+                "walker tails and group sums stay below the mask bytes");
+  // walk batch: 16 items, 8 with fp64 sums (their conversions need the
+  // registers that a wider batch would take)
+  constexpr int WB = sizeof(Acc) == sizeof(float) ? 16 : 8;
   __shared__ __align__(16) uint32_t keys[kMergedItems];
   __shared__ __align__(16) unsigned char un[kMergedUnion];
   __shared__ uint32_t dstart[kRankRadix];
@@ -600,45 +662,77 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   static_assert(NWV * kRankRadix * sizeof(uint32_t) + kMergedLr * sizeof(uint32_t) <= kMergedUnion,
                 "counters and last-read table share the union");
   const int tid = threadIdx.x, wv = tid / kWave, lane = tid % kWave;
-  if (blockIdx.x == 0 && tid == 0) *status = 0;  // the call's only kernel: no waits
+  if (blockIdx.x == 0 && tid == 0) {
+    *status = 0;  // no waits in this kernel
+    __hip_atomic_store(gate, tag << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool gated = blockIdx.x >= gate_lo && blockIdx.x < gate_hi;
+  const bool signals = blockIdx.x < gate_lo && gate_hi > gate_lo;
   const int64_t seg = xcd_block(blockIdx.x, gridDim.x);
-  if (seg >= nseg) return;  // uniform per block
+  if (seg >= nseg) {  // uniform per block
+    if (signals && tid == 0) atomicAdd(gate, 1u);
+    return;
+  }
   const int64_t b = seg / C, c = seg - (seg / C) * C;
   const int n2 = (int)(2 * T);
   const int tb1 = tbits + 1;
-  // 1. merged keys (straight to LDS), then the address passes.  A thread's
-  // address (and mask) loads are all issued before any is used.
-  constexpr int KB = ITEMS;  // items per thread (n2 <= NT * ITEMS)
-  for (int base = 0; base < n2; base += NT * KB) {
-    int64_t av[KB];
-    uint8_t mv[KB];
+  if (gated) {
+    if (tid == 0) gate_wait(gate, tag, gate_target, gate_ticks);
+    __syncthreads();
+  }
+  // 1. merged keys (straight to LDS) from the segment's address columns;
+  // thread tid takes times tid, tid + NT, ...
+  {
+    constexpr int KT = ITEMS / 2;  // times per thread (T <= NT * KT)
+    constexpr int KC = KT < 4 ? KT : 4;  // times per round of loads
+    const AddrCol wc = addr_col(waddr, wkind, b, c, T, C);
+    const AddrCol rc = addr_col(raddr, rkind, b, c, T, C);
+    // the mask through a descriptor too (no mask: an empty range), so that
+    // no load sits behind a branch
+    const __amdgpu_buffer_rsrc_t mk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(wmask ? wmask + b * T : wmask), 0, wmask ? (int)T : 0, kRsrcWord3);
+    const bool tr = trunc32 != 0;
 #pragma unroll
-    for (int m = 0; m < KB; ++m) {
-      const int i = base + m * NT + tid;
-      const int64_t t = (i < n2 ? i : 0) >> 1;
-      const bool wr = i & 1;
-      av[m] = wr ? waddr(b, t, c) : raddr(b, t, c);
-      mv[m] = (wr && wmask) ? wmask[b * T + t] : 1;
-    }
+    for (int m0 = 0; m0 < KT; m0 += KC) {
+      uint32_t wl[KC], wh[KC], rl[KC], rh[KC], mv[KC];
 #pragma unroll
-    for (int m = 0; m < KB; ++m) {
-      const int i = base + m * NT + tid;
-      if (i < n2) {
-        int64_t a = reduce_addr(av[m], A, kWrap, trunc32 != 0);
-        if (!mv[m]) a = A;
-        keys[i] = ((uint32_t)a << tb1) | (uint32_t)i;
+      for (int m = 0; m < KC; ++m) {
+        const uint32_t t = (uint32_t)((m0 + m) * NT + tid);
+        const bool ok = t < (uint32_t)T;
+        addr_col_load(wc, t, ok, &wl[m], &wh[m]);
+        addr_col_load(rc, t, ok, &rl[m], &rh[m]);
+        mv[m] = __builtin_amdgcn_raw_buffer_load_b8(mk, t, 0, 0);
+      }
+#pragma unroll
+      for (int m = 0; m < KC; ++m) {
+        const uint32_t t = (uint32_t)((m0 + m) * NT + tid);
+        if (t < (uint32_t)T) {
+          const bool keep = !wmask || mv[m] != 0;
+          const uint32_t wa =
+              keep ? (uint32_t)reduce_addr(addr_col_value(wc, t, wl[m], wh[m]), A, kWrap, tr)
+                   : (uint32_t)A;
+          const uint32_t ra =
+              (uint32_t)reduce_addr(addr_col_value(rc, t, rl[m], rh[m]), A, kWrap, tr);
+          const u32x2 kk = {(ra << tb1) | (2u * t), (wa << tb1) | (2u * t + 1u)};
+          *(u32x2*)&keys[2 * t] = kk;
+        }
       }
     }
   }
   __syncthreads();
   uint32_t (*wcnt)[kRankRadix] = (uint32_t (*)[kRankRadix])un;
+  // the rank's peer tables follow the counters (the last-read table's space)
+  uint64_t (*mt)[kRankRadix] = (uint64_t (*)[kRankRadix])(un + NWV * kRankRadix * sizeof(uint32_t));
+  static_assert(NWV * kRankRadix * (sizeof(uint32_t) + sizeof(uint64_t)) <= kMergedUnion,
+                "counters and peer tables share the union");
+  for (int i = tid; i < NWV * kRankRadix; i += NT) mt[i / kRankRadix][i % kRankRadix] = 0;
   uint32_t key[ITEMS];
   if (npass > 0) load_tile<uint32_t, ITEMS>(keys, n2, key);
   for (int p = 0; p < npass; ++p) {
     const int shift = tb1 + 8 * p;
     uint32_t rank[ITEMS];
     uint32_t own;
-    rank_tile<uint32_t, ITEMS, NT>(n2, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+    rank_tile<uint32_t, ITEMS, NT, true>(n2, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
     __syncthreads();  // dstart of every digit; every thread's keys are in registers
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -667,7 +761,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
     __syncthreads();
   }
-  const int n2r = (n2 + kWalkBatch - 1) & ~(kWalkBatch - 1);  // <= kMergedItems
+  const int n2r = (n2 + WB - 1) & ~(WB - 1);  // <= kMergedItems
   const uint32_t tmask1 = (1u << tb1) - 1u;
   {
     uint32_t cw[ITEMS];
@@ -693,10 +787,11 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
   }
   __syncthreads();
+  if (signals && tid == 0) atomicAdd(gate, 1u);  // the LDS-bound part is done
   // 3. the walk: walker w owns items [rs, re), whole batches
   const int NW = NT / G;
   const int w = tid / G, v = tid - (tid / G) * G;
-  const int len = (((n2r + NW - 1) / NW) + kWalkBatch - 1) & ~(kWalkBatch - 1);
+  const int len = (((n2r + NW - 1) / NW) + WB - 1) & ~(WB - 1);
   const int rs = w * len < n2r ? w * len : n2r;
   const int re = (rs + len) < n2r ? (rs + len) : n2r;
   // The segment's rows through buffer descriptors: row t's unit v is at byte
@@ -710,32 +805,40 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
       (void*)((const unsigned char*)payload + rbase * G * 16), 0, (int)(T * tstride), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((unsigned char*)out + rbase * G * 16), 0, (int)(T * tstride), kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t mrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(omask + rbase), 0, (int)(T * C), kRsrcWord3);
-  const uint32_t v16 = (uint32_t)v * 16u, Cu = (uint32_t)C;
-  const uint32_t mlane = v == 0 ? 0u : kCodeNoStore;  // one mask store per walker
+  const uint32_t v16 = (uint32_t)v * 16u;
+  // The reads' mask bytes gather in LDS (past the walker tails and group
+  // sums, which take at most 20 KiB) and leave in one pass at the end: byte
+  // stores amid the walk's row stores cost more than the rows.  Writes aim
+  // theirs at a spare byte past the T entries.
+  uint8_t* hm = (uint8_t*)(un + kMergedMaskOff);
   Acc acc[CPU];
   bool hasw = false;
-  // Items [i0, i1) of the range: a run start resets the sum and the has-a-
-  // write flag, a loaded write adds its row, a read (STORE) stores the sum and
-  // the flag.  The final walk streams its rows past the caches.
-  auto walk = [&](int i0, int i1, auto store_tag) {
+  // Items [from, to), in whole batches from the one holding `from` (items
+  // outside are pads): a run start resets the sum and the has-a-write flag, a
+  // loaded write adds its row, a read (STORE) stores the sum and the flag.
+  // The final walk streams the rows it reads past the caches (its stores go
+  // through L2, which measured faster than streaming them).
+  auto walk = [&](int from, int to, auto store_tag) {
     constexpr bool STORE = decltype(store_tag)::value;
     constexpr int aux = STORE ? kBufNontemporal : 0;
-    for (; i0 < i1; i0 += kWalkBatch) {
-      uint32_t cw[kWalkBatch];
+    constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
+    for (int i0 = from & ~(WB - 1); i0 < to; i0 += WB) {
+      uint32_t cw[WB];
 #pragma unroll
-      for (int q = 0; q < kWalkBatch / 4; ++q) {
+      for (int q = 0; q < WB / 4; ++q) {
         const u32x4 c4 = *(const u32x4*)&keys[i0 + 4 * q];
         cw[4 * q] = c4.x, cw[4 * q + 1] = c4.y, cw[4 * q + 2] = c4.z, cw[4 * q + 3] = c4.w;
       }
-      u32x4 x[kWalkBatch];
 #pragma unroll
-      for (int m = 0; m < kWalkBatch; ++m)
+      for (int m = 0; m < WB; ++m)
+        if (i0 + m < from || i0 + m >= to) cw[m] = kPad;
+      u32x4 x[WB];
+#pragma unroll
+      for (int m = 0; m < WB; ++m)
         x[m] = __builtin_amdgcn_raw_buffer_load_b128(
             prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad), 0, aux);
 #pragma unroll
-      for (int m = 0; m < kWalkBatch; ++m) {
+      for (int m = 0; m < WB; ++m) {
         const uint32_t k = cw[m];
         const bool st = k & kCodeStart;
 #pragma unroll
@@ -744,18 +847,47 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
         if (STORE) {
           const uint32_t ns = k & kCodeNoStore;
           __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XIn, StoreF, Acc, CPU>(acc), ors,
-                                                 (__umul24(k, tstride) + v16) | ns, 0, aux);
-          __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(hasw ? 1 : 0), mrs,
-                                               (__umul24(k, Cu) | mlane) | ns, 0, 0);
+                                                 (__umul24(k, tstride) + v16) | ns, 0, 0);
+          hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = hasw ? 1 : 0;
         }
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
         hasw = hasw || !(k & kCodeNoLoad);
       }
     }
   };
-  // tail: from the range's last run start (or its start) to its end; the
-  // batch holding that start may begin before it, whose items the start's
-  // reset discards.
+  // Run-aligned ranges: a walker with a run start in its range walks from
+  // its first one to the first start of the next walker that has one, so no
+  // run crosses walkers, and starts from zero.  When one such range would
+  // exceed 2 len (long runs), the block takes instead the fixed ranges with
+  // the tails and fold below.
+  int* astart = (int*)(un + kMergedStartOff);  // per walker: first start, -1 none
+  int a0 = n2r;
+  for (int i = rs + v; i < re; i += G)
+    if (keys[i] & kCodeStart) {
+      a0 = i;
+      break;
+    }
+  for (int o = 1; o < G; o <<= 1) {
+    const int other = __shfl_xor(a0, o, kWave);
+    a0 = other < a0 ? other : a0;
+  }
+  if (v == 0) astart[w] = a0 < re ? a0 : (rs >= n2r ? n2r : -1);
+  __syncthreads();
+  int a1 = n2r;
+  bool over = false;
+  if (a0 < re) {
+    const int n1 = w + 1 < NW ? astart[w + 1] : n2r;
+    const int n2 = w + 2 < NW ? astart[w + 2] : n2r;
+    a1 = n1 >= 0 ? n1 : n2;
+    over = a1 < 0 || a1 - a0 > 2 * len;
+  }
+  if (!__syncthreads_or(over)) {
+#pragma unroll
+    for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+    hasw = false;
+    if (a0 < re) walk(a0, a1, std::true_type{});
+  } else {
+  // tail: from the range's last run start (or its start) to its end
   int last = -1;
   for (int i = rs + v; i < re; i += G)
     if (keys[i] & kCodeStart) last = i;
@@ -765,7 +897,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   }
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
-  walk(last >= 0 ? (last & ~(kWalkBatch - 1)) : rs, re, std::false_type{});
+  walk(last >= 0 ? last : rs, re, std::false_type{});
   const bool hwt = hasw;
   const int ncol = G * CPU;  // == D
   Acc* tl = (Acc*)un;        // [walker][column]; the counters and table are dead
@@ -830,31 +962,51 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
   hasw = hwin[w] != 0;
   walk(rs, re, std::true_type{});
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t mrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(omask + rbase), 0, (int)(T * C), kRsrcWord3);
+#pragma unroll 1
+  for (int t = tid; t < T; t += NT)
+    __builtin_amdgcn_raw_buffer_store_b8(hm[t], mrs, (uint32_t)t * (uint32_t)C, 0, 0);
 }
 
 bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, const void* out) {
   const int64_t G = row_bytes / 16;
-  return tp.T >= 1 && 2 * tp.T <= kMergedItems && tp.abits + tp.tbits + 1 <= 32 &&
+  return tp.mode == kWrap && tp.T >= 1 && 2 * tp.T <= kMergedItems &&
+         tp.abits + tp.tbits + 1 <= 32 &&
          row_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
          (((uintptr_t)payload | (uintptr_t)out) & 15) == 0 && tp.nseg() <= INT32_MAX &&
          tp.C * row_bytes < ((int64_t)1 << 24) && tp.T * tp.C * row_bytes <= ((int64_t)1 << 30);
 }
 
 template <int DT>
-hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn& ra, const uint8_t* wmask,
+hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                             const void* payload, const Tape& tp, int64_t D, void* out,
                             uint8_t* omask, hipStream_t s) {
   using E = Elem<DT>;
   using S = typename E::store_t;
   using Acc = typename E::acc_t;
-  const AnyDense w{wa.dense, wa.kind, tp.T, tp.C}, r{ra.dense, ra.kind, tp.T, tp.C};
+  const AddrIn& r = ra ? *ra : wa;
   const int64_t G = D * (int64_t)sizeof(S) / 16;
   const int npass = (tp.abits + 7) / 8;
   const unsigned grid = xcd_grid(tp.nseg(), 1, (int64_t)1 << 31);
+  // the start gate: with two blocks per CU, the second of each CU waits for
+  // three quarters of the first ones' sorts (at most ~200 us)
+  int dev = 0;
+  if (hipError_t e = hipStreamGetDevice(s, &dev)) return e;
+  const DeviceShape& ds = device_shape(dev);
+  const uint32_t lo = (uint32_t)ds.cus, hi = grid < 2u * lo ? grid : 2u * lo;
+  const uint32_t gate_lo = hi > lo ? lo : grid, gate_hi = hi > lo ? hi : grid;
+  const uint32_t target = lo * 3 / 4, ticks = (uint32_t)(ds.wall_khz / 5);
+  static std::atomic<uint32_t> launches{0};
+  const uint32_t tag = (launches.fetch_add(1, std::memory_order_relaxed) + 1u) & 0xffffu;
+  uint32_t* gate = tp.status + kStatusGateWord;
 #define REM_MG(IT)                                                                           \
   segsum_merged_kernel<IT, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                     \
-      w, r, wmask, tp.T, tp.C, tp.A, tp.tbits, npass, tp.trunc32 ? 1 : 0, (int)G, tp.nseg(), \
-      (const S*)payload, (S*)out, omask, tp.status)
+      wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
+      tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
+      tag, gate_lo, gate_hi, target, ticks)
   if (2 * tp.T <= 4 * kMergedThreads)
     REM_MG(4);
   else
@@ -1022,12 +1174,11 @@ hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wma
                           const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
                           uint8_t* omask, hipStream_t s) {
   if (!tp.status) return hipErrorInvalidValue;
-  const AddrIn& r = ra ? *ra : wa;
   switch (dtype) {
-    case kF32: return seg_sum_merged_t<kF32>(wa, r, wmask, payload, tp, D, out, omask, s);
-    case kF64: return seg_sum_merged_t<kF64>(wa, r, wmask, payload, tp, D, out, omask, s);
-    case kBF16: return seg_sum_merged_t<kBF16>(wa, r, wmask, payload, tp, D, out, omask, s);
-    case kF16: return seg_sum_merged_t<kF16>(wa, r, wmask, payload, tp, D, out, omask, s);
+    case kF32: return seg_sum_merged_t<kF32>(wa, ra, wmask, payload, tp, D, out, omask, s);
+    case kF64: return seg_sum_merged_t<kF64>(wa, ra, wmask, payload, tp, D, out, omask, s);
+    case kBF16: return seg_sum_merged_t<kBF16>(wa, ra, wmask, payload, tp, D, out, omask, s);
+    case kF16: return seg_sum_merged_t<kF16>(wa, ra, wmask, payload, tp, D, out, omask, s);
     default: return hipErrorInvalidValue;
   }
 }
