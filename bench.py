@@ -48,6 +48,16 @@ def parse():
                     help="time every benchmark config (cfg1-cfg5), one JSON line per op, instead of the headline")
     ap.add_argument("--suite-parts", nargs="+", default=None, metavar="PART",
                     help="with --suite: only these parts (tapes, addresses, decode, fused)")
+    ap.add_argument("--suite-configs", nargs="+", default=None, metavar="CONFIG",
+                    help="with --suite: only these tape configs (cfg1, cfg1b, cfg2_float32, "
+                         "cfg2_bfloat16, cfg3, cfg4, cfg4_adv)")
+    ap.add_argument("--suite-ops", nargs="+", default=None, metavar="OP",
+                    help="with --suite: only these tape ops (latest_k, seg_sum)")
+    ap.add_argument("--suite-iters", type=int, default=50, help="with --suite: timed calls per op")
+    ap.add_argument("--suite-no-graphs", action="store_true",
+                    help="with --suite: time the decode step eagerly only (no HIP graph capture)")
+    ap.add_argument("--suite-calibrate", action="store_true",
+                    help="with --suite: first copy a 512 MiB tensor (a known-size kernel for counter scaling)")
     return ap.parse_args()
 
 
@@ -250,8 +260,11 @@ def main():
     if args.suite:
         from ravel_em import suite
 
-        suite.run(dev, cpu=None if args.no_cpu_baseline else suite_cpu_baseline,
-                  parts=tuple(args.suite_parts) if args.suite_parts else suite.PARTS)
+        suite.run(dev, iters=args.suite_iters,
+                  cpu=None if args.no_cpu_baseline else suite_cpu_baseline,
+                  parts=tuple(args.suite_parts) if args.suite_parts else suite.PARTS,
+                  configs=args.suite_configs, ops=args.suite_ops, calibrate=args.suite_calibrate,
+                  graphs=not args.suite_no_graphs)
         return
     log("generating cfg4 inputs on the device")
     w = workloads.cfg4(dev, adversarial=args.adversarial)

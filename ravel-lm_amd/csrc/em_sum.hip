@@ -911,43 +911,41 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   __syncthreads();
   // fold: the carry into each walker, a segmented scan over the walkers (a
   // run start resets) of the column sums and of the has-a-write flags.
-  // Thread (g, col) folds walkers [g*chunk, (g+1)*chunk) of its column, then
-  // takes the aggregates of the groups before g, then rewrites its chunk with
-  // the carries.  NG <= 64 groups keep the serial steps short.
+  // Thread (col, g) folds walkers [g*chunk, (g+1)*chunk) of its column; the
+  // NG groups of a column are consecutive lanes of one wave (NG a power of two
+  // up to 64), which scan their aggregates with shuffles; then each thread
+  // rewrites its chunk with the carries.
   {
     const int NG = (NT / ncol) < 64 ? (NT / ncol) : 64;  // >= 1 (ncol <= 512)
     const int chunk = NW / NG;
-    Acc* gsum = (Acc*)(un + (size_t)NW * ncol * sizeof(Acc));  // [NG][ncol] after tl
-    uint8_t* gflag = hwin;  // [NG] group has a run start; hwin is rewritten below
-    uint8_t* ghw = hwin + 64;  // [NG] group's has-a-write after its last start
-    const int col = tid % ncol, g = tid / ncol;
-    if (g < NG) {
-      Acc x = Acc(0);
-      bool f = false, h = false;
+    const int g = tid % NG, col = tid / NG;
+    Acc x = Acc(0);
+    bool f = false, h = false;
+    if (col < ncol) {
       for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
         const Acc t = tl[k * ncol + col];
         x = hs[k] ? t : x + t;
         h = hs[k] ? (hw[k] != 0) : (h || hw[k] != 0);
         f = f || hs[k];
       }
-      gsum[g * ncol + col] = x;
-      if (col == 0) {
-        gflag[g] = f ? 1 : 0;
-        ghw[g] = h ? 1 : 0;
-      }
     }
-    __syncthreads();
-    Acc cin = Acc(0);
-    bool hin = false;
-    if (g < NG) {
-      for (int q = 0; q < g; ++q) {
-        const Acc t = gsum[q * ncol + col];
-        cin = gflag[q] ? t : cin + t;
-        hin = gflag[q] ? (ghw[q] != 0) : (hin || ghw[q] != 0);
+    // inclusive segmented scan over the column's groups, then shift by one
+    for (int o = 1; o < NG; o <<= 1) {
+      const Acc px = __shfl_up(x, o, NG);
+      const int pf = __shfl_up((int)f, o, NG), ph = __shfl_up((int)h, o, NG);
+      if (g >= o && !f) {
+        x = px + x;
+        h = h || ph;
       }
+      f = f || (g >= o && pf);
     }
-    __syncthreads();  // the group arrays (in hwin) are read; hwin is written next
-    if (g < NG) {
+    Acc cin = __shfl_up(x, 1, NG);
+    bool hin = __shfl_up((int)h, 1, NG) != 0;
+    if (g == 0) {
+      cin = Acc(0);
+      hin = false;
+    }
+    if (col < ncol) {
       for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
         const Acc t = tl[k * ncol + col];
         tl[k * ncol + col] = cin;

@@ -59,15 +59,23 @@ def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) ->
     return out
 
 
-def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None) -> List[dict]:
+def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None,
+               ops=("latest_k", "seg_sum")) -> List[dict]:
     B, T, C, D = w.shape
     lines = []
-    us = statistics.median(time_calls(
-        lambda: causal_last_k_lookup(w.write, w.payload, w.read, address_space=w.address_space, k=w.k),
-        iters=iters))
-    lines.append(_line(w.name, "latest_k", us, workloads.algorithmic_bytes_latest_k(w), B * T,
-                       shape=[B, T, C, D], k=w.k, A=w.address_space, dtype=str(w.payload.dtype).split(".")[-1],
-                       read="separate" if w.read is not None else "same"))
+    if "latest_k" in ops:
+        us = statistics.median(time_calls(
+            lambda: causal_last_k_lookup(w.write, w.payload, w.read, address_space=w.address_space, k=w.k),
+            iters=iters))
+        lines.append(_line(w.name, "latest_k", us, workloads.algorithmic_bytes_latest_k(w), B * T,
+                           shape=[B, T, C, D], k=w.k, A=w.address_space,
+                           dtype=str(w.payload.dtype).split(".")[-1],
+                           read="separate" if w.read is not None else "same"))
+    if "seg_sum" not in ops:
+        if cpu is not None:
+            for line in lines:
+                line["cpu_baseline"] = cpu(w, line["op"])
+        return lines
     us = statistics.median(time_calls(
         lambda: causal_sum_lookup(w.write, w.payload, w.read, address_space=w.address_space), iters=iters))
     N = B * T * C
@@ -157,7 +165,7 @@ def _sum_chain(wr, payload, A):
 
 
 def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
-                 cpu: Optional[Callable] = None) -> List[dict]:
+                 cpu: Optional[Callable] = None, graphs: bool = True) -> List[dict]:
     w = workloads.cfg5(dev, steps=steps)
     B, T, H = w.prefill_write.shape
     D = w.prefill_payload.shape[-1]
@@ -183,6 +191,8 @@ def decode_lines(dev: torch.device, steps: int = 1024, graph_chunk: int = 128,
     us = statistics.median(t) / steps
     lines.append(_line("cfg5", "decode_step_eager", us, step_bytes, B, steps=steps,
                        steps_per_s=1e6 / us))
+    if not graphs:
+        return lines
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -324,22 +334,43 @@ def fused_lines(dev: torch.device, iters: int) -> List[dict]:
 PARTS = ("tapes", "addresses", "decode", "fused")
 
 
+TAPE_CONFIGS = ("cfg1", "cfg1b", "cfg2_float32", "cfg2_bfloat16", "cfg3", "cfg4", "cfg4_adv")
+TAPE_OPS = ("latest_k", "seg_sum")
+
+
 def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
-        parts=PARTS) -> List[dict]:
-    """Runs the named parts of the suite (all by default) and returns the lines."""
+        parts=PARTS, configs=None, ops=None, calibrate: bool = False,
+        graphs: bool = True) -> List[dict]:
+    """Runs the named parts of the suite (all by default) and returns the lines;
+    `configs` and `ops` narrow the tapes part to some configs and ops, and
+    `graphs=False` leaves out the decode part's HIP-graph forms.  With
+    `calibrate`, a 512 MiB device copy runs first: a kernel of known traffic
+    (512 MiB read, 512 MiB written) by which hardware byte counters are scaled."""
     lines: List[dict] = []
-    tapes = [] if "tapes" not in parts else [
-        lambda: workloads.cfg1(dev, "1"),
-        lambda: workloads.cfg1(dev, "1b"),
-        lambda: workloads.cfg2(dev, torch.float32),
-        lambda: workloads.cfg2(dev, torch.bfloat16),
-        lambda: workloads.cfg3(dev),
-        lambda: workloads.cfg4(dev),
-        lambda: workloads.cfg4(dev, adversarial=True),
-    ]
+    if calibrate:
+        src = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
+    makers = {
+        "cfg1": lambda: workloads.cfg1(dev, "1"),
+        "cfg1b": lambda: workloads.cfg1(dev, "1b"),
+        "cfg2_float32": lambda: workloads.cfg2(dev, torch.float32),
+        "cfg2_bfloat16": lambda: workloads.cfg2(dev, torch.bfloat16),
+        "cfg3": lambda: workloads.cfg3(dev),
+        "cfg4": lambda: workloads.cfg4(dev),
+        "cfg4_adv": lambda: workloads.cfg4(dev, adversarial=True),
+    }
+    bad = [c for c in (configs or ()) if c not in makers] + [o for o in (ops or ()) if o not in TAPE_OPS]
+    if bad:
+        raise ValueError(f"unknown tape configs or ops {bad}; configs {TAPE_CONFIGS}, ops {TAPE_OPS}")
+    tapes = [] if "tapes" not in parts else [makers[c] for c in TAPE_CONFIGS if not configs or c in configs]
     for make in tapes:
         w = make()
-        for line in tape_lines(w, iters, cpu):
+        for line in tape_lines(w, iters, cpu, ops=tuple(ops) if ops else TAPE_OPS):
             print(json.dumps(line), flush=True)
             lines.append(line)
         del w
@@ -356,7 +387,7 @@ def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
             lines.append(line)
         del w
         torch.cuda.empty_cache()
-    for line in decode_lines(dev, cpu=cpu) if "decode" in parts else []:
+    for line in decode_lines(dev, cpu=cpu, graphs=graphs) if "decode" in parts else []:
         print(json.dumps(line), flush=True)
         lines.append(line)
     for line in fused_lines(dev, iters) if "fused" in parts else []:
