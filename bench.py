@@ -343,10 +343,12 @@ def main():
     # payload row read per valid slot.
     gather_bytes = N * k * (4 + 1 + row_bytes) + valid_slots * row_bytes
     gather_gbps = gather_bytes / (gather_ms * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    traffic = step_measured = None
+    if os.path.exists(TRAFFIC_FILE) and not args.adversarial:  # measured for the uniform tape
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            tf = json.load(f)
+        traffic = tf.get("bytes_per_launch")
+        step_measured = tf.get("step_bytes_measured")
     op_bytes = workloads.algorithmic_bytes_latest_k(w)
     op_gbps = op_bytes / (ms * 1e-3) / 1e9
 
@@ -392,6 +394,10 @@ def main():
             "bytes_per_call": op_bytes,
             "stage_ms": stages,
             "ms_per_step_with_stage_timer": timed_ms,
+            # the step's HBM bytes from the PMC profile (FETCH/WRITE_SIZE of its
+            # kernels, scaled by the copy calibration) at this run's step time
+            "physical_bytes_per_call": step_measured,
+            "physical_frac": (step_measured / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS) if step_measured else None,
         },
         "wall_s_timed_region": wall,
         "hbm_reference_GBps": {"copy_512MiB": copy_gbps, "fill_512MiB": fill_gbps},

@@ -30,9 +30,10 @@ __device__ __forceinline__ void load_tile(const U* __restrict__ src, int n, U* k
 // forms: eight ballots (one per digit bit), or, with PEER_TABLE and a table mt
 // ([waves][256] 64-bit lane masks, all zero, left zero on return), an LDS OR
 // of each lane's bit into its digit's entry, read back, then cleared by the
-// digit's lowest lane: three LDS operations in place of some 40 VALU.  One
-// wave's LDS operations run in issue order, so the read sees every lane's OR
-// and the clear follows every read.
+// digit's lowest lane: three LDS operations in place of some 40 VALU (a wave
+// with more than 16 lanes on lane 0's digit takes the ballots).  One wave's
+// LDS operations run in issue order, so the read sees every lane's OR and the
+// clear follows every read.
 template <typename U, int ITEMS, int NT = 256, bool PEER_TABLE = false>
 __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRankRadix],
                                           uint32_t* dstart, uint32_t* scan_tmp, const U* key,
@@ -55,7 +56,11 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
     const uint32_t d = (uint32_t)(key[i] >> shift) & (kRankRadix - 1);
     uint64_t peers = 0;
     uint32_t old = 0;
-    if (PEER_TABLE) {
+    // a wave whose lanes mostly share one digit would serialize the table's
+    // ORs on one entry: it takes the ballots (wave-uniform choice)
+    const bool table =
+        PEER_TABLE && __popcll(__ballot(valid && d == __builtin_amdgcn_readfirstlane(d))) <= 16;
+    if (table) {
       if (valid) atomicOr((unsigned long long*)&mt[w][d], (unsigned long long)lane_bit);
       __builtin_amdgcn_wave_barrier();
       if (valid) {
@@ -70,7 +75,7 @@ __device__ __forceinline__ void rank_tile(int n, int shift, uint32_t (*wcnt)[kRa
     __builtin_amdgcn_wave_barrier();
     if (valid && below == 0) {  // the lowest lane of the digit advances the counter
       wcnt[w][d] = old + (uint32_t)__popcll(peers);
-      if (PEER_TABLE) mt[w][d] = 0;
+      if (table) mt[w][d] = 0;
     }
     __builtin_amdgcn_wave_barrier();
     rank[i] = old + below;

@@ -556,6 +556,7 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
@@ -578,7 +579,8 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
                        (int64_t)binbase[(seg * npass + mp) * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
+  rank_tile<U, ITEMS, kSortThreads, true>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
   gbase[tid] = (int32_t)(gofs - (int64_t)dstart[tid]);
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
@@ -648,6 +650,7 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
   constexpr int TILE = kSortThreads * ITEMS;
   static_assert(TILE * sizeof(U) >= 2 * 8 * kRadix * sizeof(uint16_t), "partial sums in stage");
   __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
@@ -679,7 +682,8 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
   const int shift = tbits + 8 * mp;
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
+  rank_tile<U, ITEMS, kSortThreads, true>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
   gbase[tid] = (int32_t)((int64_t)bef + (int64_t)base - (int64_t)dstart[tid]);
   __syncthreads();
   stage_and_write<U, ITEMS>(key, rank, n, shift, wcnt, dstart, gbase, stage, out + seg * T, T);
@@ -694,6 +698,7 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
@@ -718,7 +723,8 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   const int64_t base_d = (int64_t)binbase_p[seg * npass * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
-  rank_tile<U, ITEMS>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own);
+  for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
+  rank_tile<U, ITEMS, kSortThreads, true>(n, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
 
   // Decoupled look-back over the earlier tiles of this segment, one digit per
   // thread.  Up to kLookBatch predecessor words are read per round, so a
