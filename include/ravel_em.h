@@ -123,7 +123,9 @@ int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64
  * reference, whose library sort and scan cannot give up.
  * ravel_em_workspace_status() copies the word to *status and synchronizes
  * `stream` (not for use inside graph capture); callers that must not
- * synchronize can copy the word themselves, stream-ordered.
+ * synchronize can copy the word themselves, stream-ordered.  The rest of the
+ * header is the library's own (bytes 8..15: a start-order hint of the
+ * short-tape segmented sum; it never affects results).
  */
 #define RAVEL_EM_STATUS_BYTES 256
 enum {
