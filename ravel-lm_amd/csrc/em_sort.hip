@@ -556,11 +556,13 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
-  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
-  __shared__ U stage[TILE];
+  __shared__ __align__(16) U stage[TILE];
+  // the rank's peer tables share the staging tile (free until the ranks are done)
+  static_assert(sizeof(U) * TILE >= sizeof(uint64_t) * NW * kRadix, "peer tables fit");
+  uint64_t (*mt)[kRadix] = (uint64_t (*)[kRadix])stage;
   zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
   const int tid = threadIdx.x;
   // Consecutive tiles of a segment on one XCD: their partial output lines merge in one L2.
@@ -650,11 +652,13 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
   constexpr int TILE = kSortThreads * ITEMS;
   static_assert(TILE * sizeof(U) >= 2 * 8 * kRadix * sizeof(uint16_t), "partial sums in stage");
   __shared__ uint32_t wcnt[NW][kRadix];
-  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ __align__(16) U stage[TILE];
+  // the rank's peer tables share the staging tile (free until the ranks are done)
+  static_assert(sizeof(U) * TILE >= sizeof(uint64_t) * NW * kRadix, "peer tables fit");
+  uint64_t (*mt)[kRadix] = (uint64_t (*)[kRadix])stage;
   zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
   const int tid = threadIdx.x;
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
@@ -698,12 +702,14 @@ __global__ __launch_bounds__(kSortThreads) void sweep_kernel(
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
-  __shared__ uint64_t mt[NW][kRadix];  // rank peer tables
   __shared__ uint32_t dstart[kRadix];
   __shared__ int32_t gbase[kRadix];
   __shared__ uint32_t scan_tmp[NW + 1];
   __shared__ uint32_t s_ticket;
-  __shared__ U stage[TILE];
+  __shared__ __align__(16) U stage[TILE];
+  // the rank's peer tables share the staging tile (free until the ranks are done)
+  static_assert(sizeof(U) * TILE >= sizeof(uint64_t) * NW * kRadix, "peer tables fit");
+  uint64_t (*mt)[kRadix] = (uint64_t (*)[kRadix])stage;
   zero_slice(next_status, next_words);  // state of the next pass; every block, padding included
   // The segment comes from the (XCD-local) block id; the tile within the
   // segment from a per-segment ticket, so a tile only ever waits on tiles of
@@ -1015,7 +1021,7 @@ __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, in
 // Segments that chose the look-back link (modes[seg] == 0) run it here too:
 // the block of logical id (seg, g < ntiles) is one sweep tile of kSweepTile
 // keys on the block's 512 threads, in the same LDS.
-__global__ __launch_bounds__(kLinkThreads) void bucket_link_kernel(
+__global__ __launch_bounds__(kLinkThreads) __attribute__((amdgpu_waves_per_eu(8))) void bucket_link_kernel(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ binbase, int64_t T,
     int64_t C, int tbits, int nbuck, int ngrp, int64_t nlogical, int32_t* __restrict__ src_seg,
     const uint32_t* __restrict__ modes, uint64_t* __restrict__ status,

@@ -274,6 +274,16 @@ size_t seg_sum_status_words(const Tape& tp, int64_t D, size_t acc_size) {
 constexpr int kWalkThreads = 256;
 constexpr int kWalkBatch = 16;
 constexpr int kWalkSpin = 1 << 20;
+// Branch-free walks through buffer descriptors: a 32-bit code word per item
+// (the time in bits 0..23, flags above) and byte offsets below 2^30, so an
+// offset with bit 30 or 31 set lies past every range: the buffer unit turns
+// such a load into zeros and such a store into nothing.
+constexpr uint32_t kCodeStart = 1u << 29, kCodeNoStore = 1u << 30, kCodeNoLoad = 1u << 31;
+constexpr uint32_t kCodeTime = (1u << 24) - 1u;
+// gfx9 buffer descriptor word 3 (raw 32-bit access), and the nontemporal
+// cache-policy bit of buffer loads and stores
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kBufNontemporal = 2;
 
 template <typename Acc>
 struct Pub;
@@ -357,7 +367,7 @@ __device__ __forceinline__ void add_unit(Acc* acc, u32x4 x) {
 }
 
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT, bool FAST>
 __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int G, int64_t nparts, XOut* __restrict__ out, uint8_t* __restrict__ omask,
@@ -372,6 +382,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   __shared__ Acc tl[kWalkThreads * CPU];  // [walker][column]
   __shared__ uint32_t s_part;
   __shared__ uint8_t s_next;  // the position after the part starts a run (or the segment ends)
+  // FAST (forward exclusive sums by record, rows at 32-bit offsets of the
+  // segment's base): one code word per position, walks without branches
+  static_assert(!FAST || (!REV && !IN_SORTED && !INCL && !OUT_SORTED && !RT), "fast form");
+  __shared__ __align__(16) uint32_t cw[FAST ? kPartPos : 4];
   // Exclusive forward sums never add the last row of a run to any output:
   // those rows are not loaded (on a uniform tape most runs are one record).
   constexpr bool SKIP_LAST = !INCL && !REV;
@@ -416,9 +430,19 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   };
   const int NW = kWalkThreads / G;
   const int w = tid / G, v = tid - (tid / G) * G;
-  const int len = (n + NW - 1) / NW;
-  const int rs = w * len < n ? w * len : n;
-  const int re = (rs + len) < n ? (rs + len) : n;
+  // FAST: positions [n, nr) pad the walkers' ranges to whole batches
+  const int nr = FAST ? (n + kWalkBatch - 1) & ~(kWalkBatch - 1) : n;
+  if constexpr (FAST) {
+    for (int i = tid; i < nr; i += kWalkThreads)
+      cw[i] = i < n ? ((uint32_t)(kk[i] & tmask) | (st[i] ? kCodeStart : 0u) |
+                       (needed(i) ? 0u : kCodeNoLoad))
+                    : (kCodeNoLoad | kCodeNoStore);
+    __syncthreads();
+  }
+  const int len = FAST ? ((((nr + NW - 1) / NW) + kWalkBatch - 1) & ~(kWalkBatch - 1))
+                       : (n + NW - 1) / NW;
+  const int rs = w * len < nr ? w * len : nr;
+  const int re = (rs + len) < nr ? (rs + len) : nr;
   // Row indices fit in 32 bits (N < 2^31): record (b*T + t)*C + c, or the
   // sorted position segbase + pos.
   const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
@@ -428,27 +452,78 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   auto irow = [&](int i) -> int32_t { return IN_SORTED ? sp_of(i) : rec_of(i); };
   auto orow = [&](int i) -> int32_t { return OUT_SORTED ? sp_of(i) : rec_of(i); };
   const u32x4* inv = (const u32x4*)in;
+  // FAST: the segment's rows through buffer descriptors (row t's unit v at
+  // byte t * tstride + 16 v of the segment's base, in the payload and the
+  // output alike); the code word's bits 29..31 are flags above the time, which
+  // the 24-bit multiply ignores.
+  const uint32_t tstride = (uint32_t)(C * G * 16), v16 = (uint32_t)v * 16u;
+  const int ext = FAST ? (int)(T * C * G * 16) : 0;  // below 2^30 in the fast form
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const unsigned char*)in + (int64_t)vbase * G * 16), 0, ext, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((unsigned char*)out + (int64_t)vbase * G * 16), 0, ext, kRsrcWord3);
+  Acc acc[CPU];
+  // Items [from, to) in whole batches from the one holding `from` (items
+  // outside are pads): a run start resets the sum, every position stores the
+  // sum before its own row (STORE), every needed row is added.
+  auto walk_fast = [&](int from, int to, auto store_tag) {
+    constexpr bool STORE = decltype(store_tag)::value;
+    constexpr int aux = STORE ? kBufNontemporal : 0;
+    constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
+    if constexpr (FAST)
+    for (int i0 = from & ~(kWalkBatch - 1); i0 < to; i0 += kWalkBatch) {
+      uint32_t c4w[kWalkBatch];
+#pragma unroll
+      for (int q4 = 0; q4 < kWalkBatch / 4; ++q4) {
+        const u32x4 c4 = *(const u32x4*)&cw[i0 + 4 * q4];
+        c4w[4 * q4] = c4.x, c4w[4 * q4 + 1] = c4.y, c4w[4 * q4 + 2] = c4.z, c4w[4 * q4 + 3] = c4.w;
+      }
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m)
+        if (i0 + m < from || i0 + m >= to) c4w[m] = kPad;
+      u32x4 x[kWalkBatch];
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m)
+        x[m] = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, (__umul24(c4w[m], tstride) + v16) | (c4w[m] & kCodeNoLoad), 0, aux);
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m) {
+        const uint32_t k = c4w[m];
+        const bool stt = k & kCodeStart;
+#pragma unroll
+        for (int j = 0; j < CPU; ++j) acc[j] = stt ? Acc(0) : acc[j];
+        if (STORE)
+          __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XOut, StoreF, Acc, CPU>(acc), ors,
+                                                 (__umul24(k, tstride) + v16) | (k & kCodeNoStore), 0,
+                                                 aux);
+        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
+      }
+    }
+  };
   // 2. tail of the walker's range
   int last = -1;
   for (int i = rs + v; i < re; i += G)
-    if (st[i]) last = i;
+    if (FAST ? (cw[i] & kCodeStart) != 0 : st[i] != 0) last = i;
   for (int o = 1; o < G; o <<= 1) {
     const int other = __shfl_xor(last, o, kWave);
     last = other > last ? other : last;
   }
-  Acc acc[CPU];
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
-  for (int i0 = (last >= 0 ? last : rs); i0 < re; i0 += kWalkBatch) {
-    u32x4 x[kWalkBatch];
+  if constexpr (FAST) {
+    walk_fast(last >= 0 ? last : rs, re, std::false_type{});
+  } else {
+    for (int i0 = (last >= 0 ? last : rs); i0 < re; i0 += kWalkBatch) {
+      u32x4 x[kWalkBatch];
 #pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m) {
-      const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
-      x[m] = needed(i) ? inv[(int64_t)irow(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
+      for (int m = 0; m < kWalkBatch; ++m) {
+        const int i = (i0 + m) < re ? (i0 + m) : (re - 1);
+        x[m] = needed(i) ? inv[(int64_t)irow(i) * G + v] : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int m = 0; m < kWalkBatch; ++m)
+        if (i0 + m < re) add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
     }
-#pragma unroll
-    for (int m = 0; m < kWalkBatch; ++m)
-      if (i0 + m < re) add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);
   }
   if (v == 0) hs[w] = last >= 0 ? 1 : 0;
 #pragma unroll
@@ -503,6 +578,20 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   // non-temporal and leave L2 to the keys.
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
+  if constexpr (FAST) {
+    walk_fast(rs, re, std::true_type{});
+    if (WMASK) {  // a record's mask: some earlier record of its run (byte stores after the walk)
+      __syncthreads();
+      const __amdgpu_buffer_rsrc_t mrs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(omask + vbase), 0, (int)(T * C), kRsrcWord3);
+      for (int i = tid; i < n; i += kWalkThreads) {
+        const uint32_t k = cw[i];
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)((k & kCodeStart) ? 0 : 1), mrs,
+                                             (k & kCodeTime) * (uint32_t)C, 0, 0);
+      }
+    }
+    return;
+  }
   for (int i0 = rs; i0 < re; i0 += kWalkBatch) {
     u32x4 x[kWalkBatch];
 #pragma unroll
@@ -560,19 +649,13 @@ constexpr int kMergedLr = 4096;     // addresses of the last-read table
 // most: 1024 x 16 bytes of payload as accumulators) and the fold's group sums
 // (at most kMergedThreads accumulators)
 constexpr int kMergedUnion = 40960;
-// merged-tape code words (the time in bits 0..23)
-constexpr uint32_t kCodeStart = 1u << 29, kCodeNoStore = 1u << 30, kCodeNoLoad = 1u << 31;
-constexpr uint32_t kCodeTime = (1u << 24) - 1u;
+// merged-tape code words: the walker's (the time in bits 0..23)
 // the reads' mask bytes in the union during the final walk: T entries and a
 // spare byte, clear of the walker tails and the fold's group sums
 constexpr int kMergedMaskOff = 32768;
 // the walkers' first run starts (at most kMergedThreads ints), between the two
 constexpr int kMergedStartOff = 20480;
 static_assert(kMergedMaskOff + kMergedItems / 2 + 1 <= kMergedUnion, "mask bytes fit");
-// gfx9 buffer descriptor word 3 (raw 32-bit access), and the nontemporal
-// cache-policy bit of buffer loads and stores
-constexpr int kRsrcWord3 = 0x00020000;
-constexpr int kBufNontemporal = 2;
 
 // Start gate of the merged kernel.  With every block resident at once, all
 // blocks would sort (LDS-bound) together and then walk (HBM-bound) together.
@@ -1029,10 +1112,26 @@ hipError_t run_segsum(const U* sorted, const XIn* in, const Tape& tp, int64_t D,
     const int64_t blocks = tp.nseg() * nparts;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
     uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
-    segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK, RT>
-        <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, in, tp.T, tp.C, D, tp.tbits, (int)G,
-                                                   nparts, out, omask, walk, tickets, tp.status,
-                                                   nout);
+    // the branch-free form: forward exclusive sums by record whose rows sit at
+    // offsets below 2^30 of their segment's base (24-bit time and stride)
+    constexpr bool kFastForm = !REV && !IN_SORTED && !INCL && !OUT_SORTED && !RT &&
+                               std::is_same<XIn, XOut>::value;
+    const bool fast = kFastForm && tp.T <= ((int64_t)1 << 24) &&
+                      tp.C * in_bytes < ((int64_t)1 << 24) &&
+                      tp.T * tp.C * in_bytes <= ((int64_t)1 << 30);
+#define REM_WALK(F)                                                                              \
+  segsum_walk_kernel<U, XIn, XOut, Acc, LoadF, StoreF, REV, IN_SORTED, INCL, OUT_SORTED, WMASK, RT, \
+                     F><<<(unsigned)blocks, kWalkThreads, 0, s>>>(                                \
+      sorted, in, tp.T, tp.C, D, tp.tbits, (int)G, nparts, out, omask, walk, tickets, tp.status, nout)
+    if constexpr (kFastForm) {
+      if (fast)
+        REM_WALK(true);
+      else
+        REM_WALK(false);
+    } else {
+      REM_WALK(false);
+    }
+#undef REM_WALK
     return hipGetLastError();
   }
   const int64_t nch_seg = (tp.T + kChunk - 1) / kChunk;
