@@ -319,10 +319,30 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
   auto put = [&](int64_t av, int tl, int cl) {
     int64_t a = reduce_addr(av, A, mode, trunc32 != 0);
     if (wmask && !wmask[b * T + t0 + tl]) a = A;
-    const U u = ((U)a << tbits) | (U)(t0 + tl);
-    tile[cl * pitch + tl] = u;
-    for (int p = 0; p < nh; ++p)
-      atomicAdd(&h[cl * per + p * kRadix + ((uint32_t)(u >> (hshift + 8 * p)) & (kRadix - 1))], 1u);
+    tile[cl * pitch + tl] = ((U)a << tbits) | (U)(t0 + tl);
+  };
+  // Histogram counts of N staged keys per lane, from the store pass, whose
+  // waves read one head's keys in time order.  A wave with more than 16 lanes
+  // whose first key falls on the first lane's counter (one address dominating
+  // the tape) adds every key on that counter with one atomic, so skewed
+  // addresses do not queue on one LDS word.
+  auto count = [&](const U* u, int N, int cl) {
+    for (int p = 0; p < nh; ++p) {
+      const uint32_t base = (uint32_t)(cl * per + p * kRadix);
+      const int sh = hshift + 8 * p;
+      const uint32_t x0 = __builtin_amdgcn_readfirstlane(base + ((uint32_t)(u[0] >> sh) & (kRadix - 1)));
+      if (__popcll(__ballot(base + ((uint32_t)(u[0] >> sh) & (kRadix - 1)) == x0)) > 16) {
+        uint32_t same = 0;  // keys on x0 over the wave (wave-uniform)
+        for (int q = 0; q < N; ++q) {
+          const uint32_t x = base + ((uint32_t)(u[q] >> sh) & (kRadix - 1));
+          same += (uint32_t)__popcll(__ballot(x == x0));
+          if (x != x0) atomicAdd(&h[x], 1u);
+        }
+        if ((__ballot(1) & lanemask_lt()) == 0) atomicAdd(&h[x0], same);
+      } else {
+        for (int q = 0; q < N; ++q) atomicAdd(&h[base + ((uint32_t)(u[q] >> sh) & (kRadix - 1))], 1u);
+      }
+    }
   };
   if constexpr (VEC > 1) {
     // by_cc divides by the 16-byte units of a full head group's row here
@@ -377,18 +397,24 @@ __global__ __launch_bounds__(kPackThreads) void pack_hist_kernel(
       const int cl = i / q;
       const int tq = (i - cl * q) << 2;
       const int64_t o = (b * C + c0 + cl) * T + t0 + tq;
-      *(u32x4*)&keys[o] = *(const u32x4*)&tile[cl * pitch + tq];
+      const u32x4 w = *(const u32x4*)&tile[cl * pitch + tq];
+      *(u32x4*)&keys[o] = w;
       if (fill_src) *(u32x4*)&fill_src[o] = u32x4{~0u, ~0u, ~0u, ~0u};
+      const U k4[4] = {(U)w.x, (U)w.y, (U)w.z, (U)w.w};
+      count(k4, 4, cl);
     }
   } else {
     for (int i = threadIdx.x; i < n; i += kPackThreads) {
       const int cl = (int)fdiv_or((uint32_t)i, by_tt, (uint32_t)tt);
       const int tl = i - cl * tt;
       const int64_t o = (b * C + c0 + cl) * T + t0 + tl;
-      keys[o] = tile[cl * pitch + tl];
+      const U u = tile[cl * pitch + tl];
+      keys[o] = u;
       if (fill_src) fill_src[o] = -1;
+      count(&u, 1, cl);
     }
   }
+  __syncthreads();  // every count
   // hist layout [seg][tile][pass][256] of 16-bit counts: one contiguous run per head.
   for (int i = threadIdx.x; i < hw; i += kPackThreads) {
     const int cl = i / per;
