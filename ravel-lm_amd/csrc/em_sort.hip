@@ -525,23 +525,17 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
 
 // Pass offsets of a segment with at most kShortMaxTiles pack tiles: one block
 // per (segment, histogram pass), thread d = digit.  binbase[seg][pass][d] =
-// exclusive scan over digits of the segment's digit totals; for the first
-// noffs histogram passes (the candidates for the first scatter) also
-// offs[pass][seg][scatter tile][d] = count of digit d in the earlier scatter
-// tiles (2^lm pack tiles each).  With `modes`, the block of histogram pass 1
-// (the high digit of a two-pass key) sets modes[seg] = 1 when no bucket of
-// that digit holds more than bucket_max keys (the segment then scatters by the
-// high digit and links by buckets), else 0 (low digit first, look-back link).
-// Resets the look-back tickets of all npass passes.
+// exclusive scan over digits of the segment's digit totals; for pass 0 (the
+// first scatter) also offs[seg][scatter tile][d] = count of digit d in the
+// earlier scatter tiles (2^lm pack tiles each).  Resets the look-back tickets
+// of all npass passes.
 constexpr int kShortMaxTiles = 64;
 
 __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
     const uint16_t* __restrict__ hist, int nt0, int lm, int nh, int npass,
     uint32_t* __restrict__ offs, int nsct, uint32_t* __restrict__ binbase,
-    uint32_t* __restrict__ tickets, int64_t nseg, int noffs, uint32_t* __restrict__ modes,
-    uint32_t bucket_max) {
+    uint32_t* __restrict__ tickets, int64_t nseg) {
   __shared__ uint32_t tmp[kSortThreads / kWave + 1];
-  __shared__ uint32_t s_big;
   const int d = threadIdx.x;
   const int64_t seg = blockIdx.x / nh;
   const int p = (int)(blockIdx.x - seg * nh);
@@ -553,22 +547,15 @@ __global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
   uint32_t tot = 0;
 #pragma unroll
   for (int j = 0; j < kShortMaxTiles; ++j) tot += v[j];
-  if (modes && p == 1 && d == 0) s_big = 0;
   binbase[(seg * nh + p) * kRadix + d] = block_excl_scan<kSortThreads>(tot, tmp, nullptr);
-  if (p < noffs) {
+  if (p == 0) {
     const int mmask = (1 << lm) - 1;
-    uint32_t* op = offs + (int64_t)p * nseg * nsct * kRadix;
     uint32_t run = 0;
 #pragma unroll
     for (int j = 0; j < kShortMaxTiles; ++j) {
-      if (j < nt0 && (j & mmask) == 0) op[(seg * nsct + (j >> lm)) * kRadix + d] = run;
+      if (j < nt0 && (j & mmask) == 0) offs[(seg * nsct + (j >> lm)) * kRadix + d] = run;
       run += v[j];
     }
-  }
-  if (modes && p == 1) {  // s_big was set before the scan's barriers
-    if (tot > bucket_max) s_big = 1;
-    __syncthreads();
-    if (d == 0) modes[seg] = s_big ? 0u : 1u;
   }
   if (p == 0 && d < npass) tickets[(int64_t)d * nseg + seg] = 0;  // [pass][seg]
 }
@@ -577,8 +564,7 @@ template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint32_t* __restrict__ offs,
     const uint32_t* __restrict__ binbase, int npass, int64_t T, int ntiles, int64_t nblk,
-    int shift, uint32_t* __restrict__ zero0, int64_t zero0_words,
-    const uint32_t* __restrict__ modes, int64_t offs_pass_words) {
+    int shift, uint32_t* __restrict__ zero0, int64_t zero0_words) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ uint32_t wcnt[NW][kRadix];
@@ -598,13 +584,10 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
   const int tile = (int)(lb - seg * ntiles);
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  // modes[seg] = 1: this segment scatters by histogram pass 1 (the next digit)
-  const int mp = modes ? (int)modes[seg] : 0;
-  shift += 8 * mp;
   U key[ITEMS];
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
-  const int64_t gofs = (int64_t)offs[mp * offs_pass_words + (seg * ntiles + tile) * (int64_t)kRadix + tid] +
-                       (int64_t)binbase[(seg * npass + mp) * kRadix + tid];
+  const int64_t gofs = (int64_t)offs[(seg * ntiles + tile) * (int64_t)kRadix + tid] +
+                       (int64_t)binbase[seg * npass * kRadix + tid];
   uint32_t rank[ITEMS];
   uint32_t own;
   for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
@@ -662,18 +645,57 @@ __device__ __forceinline__ void hist_sums(const uint16_t* __restrict__ hs, int p
   __syncthreads();
 }
 
+// State of the bucket link's large buckets.  A bucket of more than kLinkPart
+// keys (one address dominating the tape) is linked in parts of kBigPart keys,
+// which the owner blocks of the segment take from the segment's queue before
+// their own buckets, so the long rounds start first.  A part gets the last
+// time of each low digit before it by a decoupled look-back over its bucket's
+// earlier parts.  Per segment, uint32 words at big + seg * hdr (written by the
+// scatter's tile-0 block):
+//   kBigTotal, kBigTicket   parts of the segment's large buckets, parts taken
+//   kBigFirst [256]         index of each large bucket's first part
+//   then [qmax]             (bucket << 16 | part number in the bucket) of part q
+// and after all headers the tables [nseg][qmax][256] (the parts' zeroed by the
+// scatter):
+// per part and low digit kBigAgg | kBigInc | kLHas32 | last time.  A part's
+// word carries kBigAgg once the part's own last time is in it and kBigInc once
+// it covers the bucket's earlier parts too.  The words are agent-scope
+// atomics, no fence (a fence writes back and invalidates the XCD's L2).  A
+// part waits only for parts taken before it, whose running blocks publish
+// them without waiting.
+constexpr int kLinkSteps = 16;
+constexpr int kLinkRun = kLinkSteps * kWave;      // keys of one wave's run
+constexpr int kLinkWaves = 8;
+constexpr int kLinkPart = kLinkWaves * kLinkRun;  // keys of one block's round
+constexpr int kBigPart = kLinkPart / 2;            // keys of a large bucket's part
+constexpr uint32_t kLHas32 = 1u << 31;            // table word: has a key | its time
+constexpr uint32_t kBigAgg = 1u << 30, kBigInc = 1u << 29;
+constexpr int kBigTotal = 0, kBigTicket = 1, kBigFirst = 2, kBigPlist = kBigFirst + kRadix;
+
+struct BigLayout {
+  int64_t nseg, qmax, hdr;  // segments, parts per segment at most, header words
+  __host__ __device__ int64_t tables() const { return nseg * hdr; }
+  __host__ __device__ int64_t table_words() const { return nseg * qmax * kRadix; }
+  __host__ __device__ int64_t words() const { return tables() + table_words(); }
+};
+// parts per segment <= T/kBigPart + large buckets <= 2 * ceil(T/kBigPart)
+__host__ __device__ inline BigLayout big_layout(int64_t T, int64_t nseg) {
+  BigLayout L;
+  L.nseg = nseg;
+  L.qmax = 2 * ((T + kBigPart - 1) / kBigPart);
+  L.hdr = kBigPlist + L.qmax;
+  return L;
+}
+
 // The pass-0 scatter of bucket mode with its offsets computed in place (no
-// offsets kernel): each block reads its segment's pack histograms of the
-// high digit, the segment's blocks all decide the same mode (bucket link when
-// no high-digit bucket exceeds bucket_max keys, else the low digit first and
-// the look-back link), and the tile-0 block publishes the scattered pass's
-// digit bases, the mode and fresh look-back tickets for the link.
+// offsets kernel): each block reads its segment's pack histograms of the high
+// digit and scatters its tile by that digit; the tile-0 block publishes the
+// bucket starts and the plan of the segment's large buckets.
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
     const U* __restrict__ in, U* __restrict__ out, const uint16_t* __restrict__ hist, int nt0,
-    int m, int64_t T, int ntiles, int64_t nblk, int tbits, uint32_t* __restrict__ zero0,
-    int64_t zero0_words, uint32_t* __restrict__ binbase, uint32_t* __restrict__ modes,
-    uint32_t* __restrict__ tickets, int npass, int64_t nseg, uint32_t bucket_max) {
+    int m, int64_t T, int ntiles, int64_t nblk, int tbits, uint32_t* __restrict__ binbase,
+    uint32_t* __restrict__ big, int64_t nseg) {
   constexpr int NW = kSortThreads / kWave;
   constexpr int TILE = kSortThreads * ITEMS;
   static_assert(TILE * sizeof(U) >= 2 * 8 * kRadix * sizeof(uint16_t), "partial sums in stage");
@@ -685,31 +707,37 @@ __global__ __launch_bounds__(kSortThreads) void scatter0_bucket_kernel(
   // the rank's peer tables share the staging tile (free until the ranks are done)
   static_assert(sizeof(U) * TILE >= sizeof(uint64_t) * NW * kRadix, "peer tables fit");
   uint64_t (*mt)[kRadix] = (uint64_t (*)[kRadix])stage;
-  zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
   const int tid = threadIdx.x;
+  const BigLayout L = big_layout(T, nseg);
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   if (lb >= nblk) return;  // uniform per block
   const int64_t seg = lb / ntiles;
   const int tile = (int)(lb - seg * ntiles);
   const int64_t start = (int64_t)tile * TILE;
   const int n = (int)((T - start) < TILE ? (T - start) : TILE);
-  constexpr int nh = 2;  // histogram passes: the low and the high digit
-  const int per = nh * kRadix;
-  const uint16_t* hs = hist + seg * (int64_t)nt0 * per;
+  const uint16_t* hs = hist + seg * (int64_t)nt0 * kRadix;
   U key[ITEMS];
   load_tile<U, ITEMS>(in + seg * T + start, n, key);
   uint32_t bef, tot;
-  hist_sums<kSortThreads>(hs + kRadix, per, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
-  const int big = __syncthreads_or(tot > bucket_max);
-  const int mp = big ? 0 : 1;  // the digit this segment scatters by (1 = high)
-  if (!mp) hist_sums<kSortThreads>(hs, per, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
+  hist_sums<kSortThreads>(hs, kRadix, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
   const uint32_t base = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
   if (tile == 0) {
-    binbase[(seg * nh + mp) * kRadix + tid] = base;
-    if (tid == 0) modes[seg] = (uint32_t)mp;
-    if (tid < npass) tickets[(int64_t)tid * nseg + seg] = 0;  // [pass][seg]
+    binbase[seg * kRadix + tid] = base;
+    // large buckets: parts of kBigPart keys, numbered bucket by bucket
+    uint32_t* hdr = big + seg * L.hdr;
+    const uint32_t parts = tot > (uint32_t)kLinkPart ? (tot + kBigPart - 1) / kBigPart : 0u;
+    uint32_t total;
+    const uint32_t pb = block_excl_scan<kSortThreads>(parts, scan_tmp, &total);
+    hdr[kBigFirst + tid] = pb;
+    for (uint32_t j = 0; j < parts; ++j) hdr[kBigPlist + pb + j] = ((uint32_t)tid << 16) | j;
+    if (tid == 0) {
+      hdr[kBigTotal] = total;
+      hdr[kBigTicket] = 0;
+    }
+    uint32_t* tw = big + L.tables() + seg * L.qmax * kRadix;  // the parts' tables start unpublished
+    for (uint32_t i = tid; i < total * kRadix; i += kSortThreads) tw[i] = 0;
   }
-  const int shift = tbits + 8 * mp;
+  const int shift = tbits + 8;
   uint32_t rank[ITEMS];
   uint32_t own;
   for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
@@ -819,8 +847,7 @@ constexpr uint64_t kLFlagP = 2ull << 62;
 constexpr uint64_t kLHasKey = 1ull << 61;
 constexpr uint64_t kLCountMask = (1ull << 29) - 1;
 
-// One tile of the link sweep on NT threads (the standalone kernel runs 256,
-// the bucket link's look-back segments 512); the LDS arrays come from the
+// One tile of the link sweep on NT threads; the LDS arrays come from the
 // caller.
 template <int ITEMS, int NT>
 __device__ __forceinline__ void sweep_link_tile(
@@ -964,21 +991,21 @@ __global__ __launch_bounds__(kSortThreads) void sweep_link_kernel(
 // A wave's LDS operations execute in issue order, so every read sees exactly
 // the writes of earlier steps and of this step's earlier instructions.
 //
-// The block of logical id (seg, g) owns buckets 8g..8g+7 of segment seg.
-// A bucket of at most kLinkRun keys is one run of one wave (wave w takes
+// The block of logical id (seg, g < ngrp) owns buckets 8g..8g+7 of segment
+// seg.  A bucket of at most kLinkRun keys is one run of one wave (wave w takes
 // bucket 8g + w; uniform addresses put ~T/256 keys in a bucket).  A larger
-// bucket is walked by all 8 waves of the block together, in rounds of 8
-// runs: after a round a block barrier, then per digit the last time before
-// each wave's run (from earlier waves' tables and a running carry over the
-// rounds), then each wave resolves the keys of its run that had no
-// predecessor inside the run.  No look-back, no wait on another block.  A
-// segment with a bucket of more than one round's keys links by look-back
-// instead (the offsets kernel decides).
-constexpr int kLinkWaves = 8;
+// bucket is walked by all 8 waves of a block together, one round of 8 runs
+// (kLinkPart keys): after the round a block barrier, then per digit the last
+// time before each wave's run (from earlier waves' tables), then each wave
+// resolves the keys of its run that had no predecessor inside the run.
+// A bucket of more than kLinkPart keys (one address dominating the tape) has
+// parts of kBigPart keys (runs of kBigPart / 8 keys per wave): the owner walks
+// part 0, other blocks the later parts, all at once.  Each part publishes, per low digit, the time
+// of its first key that found no predecessor inside the part and its last
+// time; the segment's last part to finish (a counter, no block waits on
+// another) then gives each such first key the last time of its digit in the
+// bucket's earlier parts.
 constexpr int kLinkThreads = kLinkWaves * kWave;
-constexpr int kLinkSteps = 16;
-constexpr int kLinkRun = kLinkSteps * kWave;  // keys of one wave's run
-constexpr uint32_t kLHas32 = 1u << 31;        // table word: has a key | its time
 
 template <bool COOP>
 __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, int64_t start,
@@ -1044,90 +1071,171 @@ __device__ __forceinline__ uint32_t link_run(const uint32_t* __restrict__ kk, in
   return first;
 }
 
-// Segments that chose the look-back link (modes[seg] == 0) run it here too:
-// the block of logical id (seg, g < ntiles) is one sweep tile of kSweepTile
-// keys on the block's 512 threads, in the same LDS.
 __global__ __launch_bounds__(kLinkThreads) __attribute__((amdgpu_waves_per_eu(8))) void bucket_link_kernel(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ binbase, int64_t T,
     int64_t C, int tbits, int nbuck, int ngrp, int64_t nlogical, int32_t* __restrict__ src_seg,
-    const uint32_t* __restrict__ modes, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ ticket, int ntiles, uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ big, int64_t nseg, uint32_t* __restrict__ err) {
   __shared__ __align__(16) uint64_t mtab[kLinkWaves][kRadix];  // all zero between steps
   __shared__ __align__(16) uint32_t ltab[kLinkWaves][kRadix];  // kLHas32 | time, 0 = none
   __shared__ __align__(16) uint32_t ctab[kLinkWaves][kRadix];  // carry into a wave's run
-  __shared__ uint32_t runc[kRadix];  // carry after the rounds so far
+  __shared__ uint32_t runc[kRadix];  // last time of each digit in the round
+  __shared__ uint32_t ftab[kRadix];  // first time of each digit left without a predecessor
   __shared__ uint32_t bstart[kLinkWaves + 1];
+  __shared__ uint32_t s_part;
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
   const int64_t logical = xcd_block(blockIdx.x, gridDim.x);
-  if (logical >= nlogical) return;  // uniform per block
-  const int64_t seg = logical / ngrp;
-  const int g = (int)(logical - seg * ngrp);
-  if (!modes[seg]) {  // uniform per block: this segment links by look-back
-    static_assert(kLinkThreads * (kSweepTile / kLinkThreads) == kSweepTile, "sweep tile");
-    static_assert(sizeof(mtab) >= kSweepTile * sizeof(uint32_t), "stage in mtab");
-    static_assert(sizeof(ctab) >= 4 * kRadix * sizeof(uint32_t), "small arrays in ctab");
-    if (g >= ntiles) return;
-    sweep_link_tile<kSweepTile / kLinkThreads, kLinkThreads>(
-        keys, status, ticket, T, C, ntiles, seg, tbits + 8, tbits, err, src_seg, ltab, ctab[0],
-        ctab[3], &ctab[4][0], ctab[1], (uint8_t*)ctab[2], (uint32_t*)&mtab[0][0]);
-    return;
-  }
-  const int b0 = g * kLinkWaves;
-  const uint32_t* bb = binbase + (seg * 2 + 1) * kRadix;  // the high digit's bucket starts
-  if (tid <= kLinkWaves) {
-    const int x = b0 + tid;
-    bstart[tid] = x < nbuck ? bb[x] : (x < kRadix ? bb[x] : (uint32_t)T);
-  }
+  const BigLayout L = big_layout(T, nseg);
   uint64_t* mt = mtab[w];
   uint32_t* lt = ltab[w];
 #pragma unroll
   for (int i = 0; i < kRadix / kWave; ++i) mt[i * kWave + lane] = 0;
-  __syncthreads();
-  const uint32_t* kk = keys + seg * T;
-  const int64_t b = seg / C, c = seg - (seg / C) * C;
-  const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
-  int32_t* dst = src_seg + seg * T;
   const uint32_t tmask = (1u << tbits) - 1u;
   uint32_t u[kLinkSteps];
-  // Small buckets: one wave each.
+  // One round over keys [r0, r1) (at most kLinkWaves * run) of segment seg's
+  // bucket, a run of keys per wave.  Keys without a predecessor in the round
+  // keep the pre-filled -1, or with `part` are left in ftab for the part's
+  // look-back.
+  auto round = [&](int64_t seg, int64_t r0, int64_t r1, int run, bool part) {
+    const uint32_t* kk = keys + seg * T;
+    const int64_t b = seg / C, c = seg - (seg / C) * C;
+    const int32_t vbase = (int32_t)((b * T) * C + c), Ci = (int32_t)C;
+    int32_t* dst = src_seg + seg * T;
+    const int64_t s0 = r0 + (int64_t)w * run;
+    const int64_t e0 = (s0 + run) < r1 ? (s0 + run) : r1;
+    uint32_t first = 0;
+    if (s0 < e0) {
+      first = link_run<true>(kk, s0, e0, tbits, mt, lt, vbase, Ci, dst, u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kRadix / kWave; ++i) lt[i * kWave + lane] = 0;
+    }
+    __syncthreads();  // every wave's last times
+    if (tid < kRadix) {
+      uint32_t cy = 0;
+#pragma unroll
+      for (int v = 0; v < kLinkWaves; ++v) {
+        ctab[v][tid] = cy;
+        const uint32_t l = ltab[v][tid];
+        if (l) cy = l;
+      }
+      runc[tid] = cy;
+      ftab[tid] = 0;
+    }
+    __syncthreads();  // every wave's carries
+#pragma unroll
+    for (int st = 0; st < kLinkSteps; ++st) {
+      if ((first >> st) & 1u) {
+        const uint32_t d = (u[st] >> tbits) & (kRadix - 1);
+        const uint32_t cy = ctab[w][d];
+        if (cy)
+          dst[u[st] & tmask] = vbase + (int32_t)(cy & ~kLHas32) * Ci;
+        else if (part)  // the digit's first key in the part (one per digit)
+          ftab[d] = kLHas32 | (u[st] & tmask);
+      }
+    }
+    __syncthreads();  // ftab complete, ctab free
+  };
+  if (logical >= nlogical) return;  // padding block (uniform)
+  const int64_t oseg = logical / ngrp;  // the segment of the buckets this block owns
+  const int b0 = (int)(logical - oseg * ngrp) * kLinkWaves;
   {
-    const int64_t lo = bstart[w], hi = bstart[w + 1];
-    if (b0 + w < nbuck && hi - lo <= kLinkRun)
-      link_run<false>(kk, lo, hi, tbits, mt, lt, vbase, Ci, dst, u);
+    const uint32_t* bb = binbase + oseg * kRadix;
+    if (tid <= kLinkWaves) {
+      const int x = b0 + tid;
+      bstart[tid] = x < kRadix ? bb[x] : (uint32_t)T;
+    }
   }
-  // Large buckets: the block's waves together (block-uniform loop).
-  for (int x = 0; x < kLinkWaves; ++x) {
-    const int64_t lo = bstart[x], hi = bstart[x + 1];
-    if (b0 + x >= nbuck || hi - lo <= kLinkRun) continue;
-    for (int64_t r0 = lo; r0 < hi; r0 += (int64_t)kLinkWaves * kLinkRun) {
-      const int64_t s0 = r0 + (int64_t)w * kLinkRun;
-      const int64_t e0 = (s0 + kLinkRun) < hi ? (s0 + kLinkRun) : hi;
-      uint32_t first = 0;
-      if (s0 < e0) {
-        first = link_run<true>(kk, s0, e0, tbits, mt, lt, vbase, Ci, dst, u);
-      } else {
-#pragma unroll
-        for (int i = 0; i < kRadix / kWave; ++i) lt[i * kWave + lane] = 0;
+  // First the parts of the segment's large buckets, from its queue, in order.
+  {
+    const int64_t seg = oseg;
+    uint32_t* hdr = big + seg * L.hdr;
+    const uint32_t nq = hdr[kBigTotal];  // loaded with the bucket starts
+    for (bool again = false; nq; again = true) {  // block-uniform
+      if (tid == 0) {
+        // after a part, a plain look first: a drained queue's counter stays put
+        uint32_t t = again ? __hip_atomic_load(&hdr[kBigTicket], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)
+                           : 0u;
+        if (t < nq) t = atomicAdd(&hdr[kBigTicket], 1u);
+        s_part = t;
       }
-      __syncthreads();  // every wave's last times
+      __syncthreads();
+      const int q = (int)s_part;
+      __syncthreads();  // s_part read by all before the next ticket
+      if (q >= (int)nq) break;
+      const uint32_t xj = hdr[kBigPlist + q];
+      const int x = (int)(xj >> 16), j = (int)(xj & 0xffff);
+      const uint32_t* bb = binbase + seg * kRadix;
+      const int64_t lo = (int64_t)bb[x] + (int64_t)j * kBigPart;
+      const int64_t hi = x + 1 < kRadix ? (int64_t)bb[x + 1] : T;
+      round(seg, lo, (lo + kBigPart) < hi ? lo + kBigPart : hi, kBigPart / kLinkWaves, true);
       if (tid < kRadix) {
-        uint32_t cy = r0 == lo ? 0u : runc[tid];
+        uint32_t* tw = big + L.tables() + (seg * L.qmax + q) * kRadix;  // [seg][q] tables
+        const uint32_t own = runc[tid];  // kLHas32 | last time, or 0
+        if (j == 0) {
+          __hip_atomic_store(&tw[tid], kBigAgg | kBigInc | own, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          __hip_atomic_store(&tw[tid], kBigAgg | own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // look back over parts j-1 .. 0 of the bucket for the digit's last
+          // time, kBigBatch predecessor words read at once
+          constexpr int kBigBatch = 8;
+          uint32_t cy = 0;
+          bool ok = true, done = false;
+          for (int j0 = 1; j0 <= j && !done; j0 += kBigBatch) {
+            uint32_t v[kBigBatch];
 #pragma unroll
-        for (int v = 0; v < kLinkWaves; ++v) {
-          ctab[v][tid] = cy;
-          const uint32_t l = ltab[v][tid];
-          if (l) cy = l;
-        }
-        runc[tid] = cy;
-      }
-      __syncthreads();  // every wave's carries
+            for (int i = 0; i < kBigBatch; ++i)
+              v[i] = j0 + i <= j ? __hip_atomic_load(&tw[tid - (int64_t)(j0 + i) * kRadix],
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : kBigAgg | kBigInc;
 #pragma unroll
-      for (int st = 0; st < kLinkSteps; ++st) {
-        if ((first >> st) & 1u) {
-          const uint32_t cy = ctab[w][(u[st] >> tbits) & (kRadix - 1)];
-          if (cy) dst[u[st] & tmask] = vbase + (int32_t)(cy & ~kLHas32) * Ci;  // else pre-filled -1
+            for (int i = 0; i < kBigBatch; ++i) {
+              if (done) break;
+              const uint32_t* pw = tw - (int64_t)(j0 + i) * kRadix;
+              for (int spins = 0; !(v[i] & kBigAgg) && spins < kSpinLimit; ++spins) {
+                __builtin_amdgcn_s_sleep(1);
+                v[i] = __hip_atomic_load(&pw[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+              if (!(v[i] & kBigAgg)) {
+                ok = false;
+                done = true;
+              } else if ((v[i] & kLHas32) || (v[i] & kBigInc)) {
+                cy = v[i] & (kLHas32 | tmask);  // has | time, or 0 from an inclusive word without
+                done = true;
+              }
+            }
+          }
+          if (!ok) atomicOr(err, kStatusSortWait);
+          __hip_atomic_store(&tw[tid], kBigAgg | kBigInc | (own ? own : cy), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          const uint32_t f = ftab[tid];
+          if (f && cy) {
+            const int64_t b = seg / C, c = seg - (seg / C) * C;
+            src_seg[seg * T + (f & tmask)] =
+                (int32_t)((b * T) * C + c) + (int32_t)(cy & ~kLHas32) * (int32_t)C;
+          }
         }
       }
+    }
+  }
+  {  // then the 8 buckets this block owns
+    const int64_t seg = oseg;
+    __syncthreads();  // bstart
+    // Small buckets: one wave each.
+    {
+      const int64_t lo = bstart[w], hi = bstart[w + 1];
+      if (b0 + w < nbuck && hi - lo <= kLinkRun) {
+        const int64_t b = seg / C, c = seg - (seg / C) * C;
+        link_run<false>(keys + seg * T, lo, hi, tbits, mt, lt, (int32_t)((b * T) * C + c),
+                        (int32_t)C, src_seg + seg * T, u);
+      }
+    }
+    // Larger buckets up to one round: the block's waves together (block-uniform).
+    for (int x = 0; x < kLinkWaves; ++x) {
+      const int64_t lo = bstart[x], hi = bstart[x + 1];
+      if (b0 + x < nbuck && hi - lo > kLinkRun && hi - lo <= kLinkPart)
+        round(seg, lo, hi, kLinkRun, false);
     }
   }
 }
@@ -1204,8 +1312,8 @@ size_t sort_fused_words(const Tape& tp, size_t key_bytes) {
   const int64_t offs = tp.nseg() * scatter0_tiles(tp) * kRadix;
   const int64_t bins = tp.nseg() * npass * kRadix;
   const int64_t status = tp.nseg() * sweep_tiles(tp) * kRadix;
-  // bucket mode: offsets of two candidate first digits and the segment modes
-  const int64_t bucket = bucket_mode(tp, key_bytes, nt0) ? offs + tp.nseg() : 0;
+  // bucket mode: the state of the link's large buckets
+  const int64_t bucket = bucket_mode(tp, key_bytes, nt0) ? big_layout(tp.T, tp.nseg()).words() : 0;
   // two look-back status buffers, each room for one 64-bit word per entry
   return (size_t)(hist + offs + bins + 4 * status + (npass + 1) * tp.nseg() + bucket);
 }
@@ -1222,16 +1330,16 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   const int nsct = (int)scatter0_tiles(tp);
   const int m = (kSortThreads * kScatter0Items) / tt;  // pack tiles per scatter tile
   // With link_seg and 32-bit keys the last pass links instead of sorting and
-  // needs no digit offsets.  With two passes and short segments each segment
-  // picks its link on the device (bucket_mode): by buckets of the high digit
-  // after one scatter by that digit, unless a bucket is too large for one
-  // block, then by look-back after a scatter by the low digit.
+  // needs no digit offsets.  With two passes and short segments (bucket_mode)
+  // one scatter by the high digit leaves buckets that the link walks in time
+  // order; only the high digit is counted.
   const bool fuse_link = link_seg && sizeof(U) == 4 && npass >= 2;
   const bool bucket = bucket_mode(tp, sizeof(U), nt0) && fuse_link;
-  const int nh = bucket ? npass : (fuse_link ? npass - 1 : npass);
+  const int nh = bucket ? 1 : (fuse_link ? npass - 1 : npass);
+  const int h0 = bucket ? 1 : 0;  // first counted digit
   const int64_t hist_words = tp.nseg() * nt0 * nh * kRadix;
   const int64_t offs_pass = tp.nseg() * nsct * kRadix;
-  const int64_t offs_words = offs_pass * (bucket ? 2 : 1);
+  const int64_t offs_words = bucket ? 0 : offs_pass;
   const int64_t bin_words = tp.nseg() * nh * kRadix;
   const int nts = (int)sweep_tiles(tp);
   const int64_t entries = tp.nseg() * nts * kRadix;  // look-back entries of one pass
@@ -1243,7 +1351,7 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   uint32_t* status[2] = {binbase + bin_words, binbase + bin_words + status_words};
   uint32_t* tickets = status[1] + status_words;  // [npass][nseg] tickets, then a spare row
   uint32_t* err = tp.status;  // bounded waits that give up set kStatusSortWait here
-  uint32_t* modes = bucket ? tickets + (int64_t)(npass + 1) * tp.nseg() : nullptr;
+  uint32_t* big = bucket ? tickets + (int64_t)(npass + 1) * tp.nseg() : nullptr;
   const int64_t nlogical = tp.B * nt0 * ncg;
   const unsigned pgrid = xcd_grid(nlogical, 1, (int64_t)1 << 31);
   // Divisors of the pack index math (the last head group / time tile of a row
@@ -1257,12 +1365,12 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
                      (pl.CC * (int64_t)sizeof(AT)) % 16 == 0;
     if (vec) {
       pack_hist_kernel<U, AT, VEC><<<pgrid, kPackThreads, 0, s>>>(
-          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
+          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, h0,
           nh, nt0, nlogical, make_fastdiv((uint32_t)(pl.CC / VEC)), by_tt, ka, hist, zero,
           zero_words, tp.status, bucket ? link_seg : nullptr);
     } else {
       pack_hist_kernel<U, AT, 1><<<pgrid, kPackThreads, 0, s>>>(
-          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, 0,
+          src, wmask, tp.T, tp.C, tp.A, tp.tbits, tp.mode, tp.trunc32 ? 1 : 0, tt, pl.CC, ncg, h0,
           nh, nt0, nlogical, make_fastdiv((uint32_t)pl.CC), by_tt, ka, hist, zero, zero_words,
           tp.status, bucket ? link_seg : nullptr);
     }
@@ -1278,32 +1386,28 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   uint32_t* next0 = npass > 1 ? status[0] : nullptr;
   if (bucket) {  // bucket_mode() implies nt0 <= kShortMaxTiles and two passes
     scatter0_bucket_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
-        ka, kb, hist, nt0, m, tp.T, nsct, nblk0, tp.tbits, next0, status_words, binbase, modes,
-        tickets, npass, tp.nseg(), (uint32_t)(kLinkWaves * kLinkRun));
+        ka, kb, hist, nt0, m, tp.T, nsct, nblk0, tp.tbits, binbase, big, tp.nseg());
   } else if (nt0 <= kShortMaxTiles) {
     const int lm = __builtin_ctz((unsigned)m);
     seg_offsets_kernel<<<(unsigned)(tp.nseg() * nh), kSortThreads, 0, s>>>(
-        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg(), 1, nullptr,
-        (uint32_t)(kLinkWaves * kLinkRun));
+        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg());
   } else {
     scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, nh, npass, offs, nsct,
                                                            binbase, tickets);
   }
   if (!bucket)
     scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
-        ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words, nullptr,
-        offs_pass);
+        ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (bucket) {
-    // one launch for both links: buckets for most segments, look-back tiles for the rest
+    // owners of 8 buckets each, then the later parts of large buckets
     const int nbuck = 1 << (tp.abits - 8);
-    int ngrp = (nbuck + kLinkWaves - 1) / kLinkWaves;
-    if (ngrp < nts) ngrp = nts;
+    const int ngrp = (nbuck + kLinkWaves - 1) / kLinkWaves;
     const int64_t nlog = tp.nseg() * ngrp;
     bucket_link_kernel<<<xcd_grid(nlog, 1, (int64_t)1 << 31), kLinkThreads, 0, s>>>(
-        (const uint32_t*)kb, binbase, tp.T, tp.C, tp.tbits, nbuck, ngrp, nlog, link_seg, modes,
-        (uint64_t*)status[0], tickets + tp.nseg(), nts, err);
+        (const uint32_t*)kb, binbase, tp.T, tp.C, tp.tbits, nbuck, ngrp, nlog, link_seg, big,
+        tp.nseg(), err);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     *sorted = nullptr;

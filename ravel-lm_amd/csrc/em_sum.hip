@@ -273,6 +273,7 @@ size_t seg_sum_status_words(const Tape& tp, int64_t D, size_t acc_size) {
 // blocks already claimed.
 constexpr int kWalkThreads = 256;
 constexpr int kWalkBatch = 16;
+constexpr int kFastBatch = 16;  // items a lane has in flight in the branch-free walks
 constexpr int kWalkSpin = 1 << 20;
 // Branch-free walks through buffer descriptors: a 32-bit code word per item
 // (the time in bits 0..23, flags above) and byte offsets below 2^30, so an
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   const int NW = kWalkThreads / G;
   const int w = tid / G, v = tid - (tid / G) * G;
   // FAST: positions [n, nr) pad the walkers' ranges to whole batches
-  const int nr = FAST ? (n + kWalkBatch - 1) & ~(kWalkBatch - 1) : n;
+  const int nr = FAST ? (n + kFastBatch - 1) & ~(kFastBatch - 1) : n;
   if constexpr (FAST) {
     for (int i = tid; i < nr; i += kWalkThreads)
       cw[i] = i < n ? ((uint32_t)(kk[i] & tmask) | (st[i] ? kCodeStart : 0u) |
@@ -439,7 +440,7 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
                     : (kCodeNoLoad | kCodeNoStore);
     __syncthreads();
   }
-  const int len = FAST ? ((((nr + NW - 1) / NW) + kWalkBatch - 1) & ~(kWalkBatch - 1))
+  const int len = FAST ? ((((nr + NW - 1) / NW) + kFastBatch - 1) & ~(kFastBatch - 1))
                        : (n + NW - 1) / NW;
   const int rs = w * len < nr ? w * len : nr;
   const int re = (rs + len) < nr ? (rs + len) : nr;
@@ -471,23 +472,23 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     constexpr int aux = STORE ? kBufNontemporal : 0;
     constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
     if constexpr (FAST)
-    for (int i0 = from & ~(kWalkBatch - 1); i0 < to; i0 += kWalkBatch) {
-      uint32_t c4w[kWalkBatch];
+    for (int i0 = from & ~(kFastBatch - 1); i0 < to; i0 += kFastBatch) {
+      uint32_t c4w[kFastBatch];
 #pragma unroll
-      for (int q4 = 0; q4 < kWalkBatch / 4; ++q4) {
+      for (int q4 = 0; q4 < kFastBatch / 4; ++q4) {
         const u32x4 c4 = *(const u32x4*)&cw[i0 + 4 * q4];
         c4w[4 * q4] = c4.x, c4w[4 * q4 + 1] = c4.y, c4w[4 * q4 + 2] = c4.z, c4w[4 * q4 + 3] = c4.w;
       }
 #pragma unroll
-      for (int m = 0; m < kWalkBatch; ++m)
+      for (int m = 0; m < kFastBatch; ++m)
         if (i0 + m < from || i0 + m >= to) c4w[m] = kPad;
-      u32x4 x[kWalkBatch];
+      u32x4 x[kFastBatch];
 #pragma unroll
-      for (int m = 0; m < kWalkBatch; ++m)
+      for (int m = 0; m < kFastBatch; ++m)
         x[m] = __builtin_amdgcn_raw_buffer_load_b128(
             prs, (__umul24(c4w[m], tstride) + v16) | (c4w[m] & kCodeNoLoad), 0, aux);
 #pragma unroll
-      for (int m = 0; m < kWalkBatch; ++m) {
+      for (int m = 0; m < kFastBatch; ++m) {
         const uint32_t k = c4w[m];
         const bool stt = k & kCodeStart;
 #pragma unroll

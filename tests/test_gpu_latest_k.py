@@ -351,10 +351,11 @@ def test_fused_and_generic_sorts_agree(device, shape):
 # ------------------------------------------ buckets that span many pieces --
 # With two 8-bit address digits, k = 1 and reads = writes, the link groups each
 # stream's records by the high address digit (a bucket): one wave walks a
-# bucket of up to 1024 records, a block of 8 waves a bucket of up to 8192,
-# and a stream with a larger bucket is linked by the look-back sweep instead.
-# These cases put many records into few buckets, at those boundaries, and mix
-# both kinds of stream in one call.
+# bucket of up to 1024 records, a block of 8 waves a bucket of up to 8192, and
+# a larger bucket goes in parts of 8192 records to separate blocks, whose
+# last one to finish carries each low digit's last time from part to part.
+# These cases put many records into few buckets, at those boundaries, with
+# digits missing from whole parts, and several large buckets per stream.
 
 def _hot_case(name, T, A, C=2, B=2):
     g = torch.Generator().manual_seed(T + A + len(name))
@@ -371,9 +372,13 @@ def _hot_case(name, T, A, C=2, B=2):
         w = torch.where(torch.rand(B, T, C, generator=g) < 0.9, torch.zeros_like(w), w)
     elif name == "few_buckets":  # A = 512: two buckets of ~T/2 records
         w = torch.randint(0, A, (B, T, C), generator=g)
-    elif name == "mixed_modes":  # head 0 one hot address, head 1 uniform: both links in one call
+    elif name == "mixed_modes":  # head 0 one hot address, head 1 uniform
         w = torch.randint(0, A, (B, T, C), generator=g)
         w[:, :, 0] = 11
+    elif name == "two_hot_groups":  # hot buckets 0 and 200 (different owner blocks), some spread
+        w = torch.where(torch.rand(B, T, C, generator=g) < 0.5, 7, 200 * 256 + 9)
+        r = torch.randint(0, A, (B, T, C), generator=g)
+        w = torch.where(torch.rand(B, T, C, generator=g) < 0.05, r, w)
     else:
         raise ValueError(name)
     return w
@@ -383,7 +388,8 @@ HOT = [("one_address", 1024, 4096), ("one_address", 1025, 4096), ("one_address",
        ("one_address", 8192, 4096), ("one_address", 8193, 4096), ("one_address", 16385, 4096),
        ("one_address", 70000 // 2, 65536), ("two_digits_one_bucket", 5000, 256 * 256),
        ("rare_digit", 20000, 4096), ("skewed", 30000, 65536), ("few_buckets", 40000, 512),
-       ("few_buckets", 3000, 300)]
+       ("few_buckets", 3000, 300), ("mixed_modes", 30000, 65536),
+       ("two_hot_groups", 40000, 65536)]
 
 
 @pytest.mark.parametrize("case", HOT, ids=[f"{n}-{T}-{A}" for n, T, A in HOT])
