@@ -244,14 +244,14 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
 }
 
 // ------------------------------------------------------------------------
-// Fused path.  pack_hist -> seg_offsets or scan_hist -> scatter0 (pass 0,
-// reduce-then-scan) -> sweep (passes >= 1, decoupled look-back).  Used when the per-block LDS
-// budget below holds; the generic path above handles every other shape.
-// The read == write, k == 1 link of 32-bit keys rides on the last pass
-// (sweep_link_kernel).  With exactly two digit passes and short segments each
-// segment chooses on the device: scatter by the high digit and link inside its
-// buckets (bucket_link_kernel), or, when a bucket is too large for one block,
-// scatter by the low digit and link in the look-back sweep.
+// Fused path.  pack_hist -> scatter0 (pass 0; short segments sum their tile
+// histograms in the scatter itself, longer ones after scan_hist) -> sweep
+// (passes >= 1, decoupled look-back).  Used when the per-block LDS budget
+// below holds; the generic path above handles every other shape.  The
+// read == write, k == 1 link of 32-bit keys rides on the last pass
+// (sweep_link_kernel); with exactly two digit passes and short segments one
+// scatter by the high digit is followed by the link inside its buckets
+// (bucket_link_kernel) instead.
 
 constexpr int kPackThreads = 512;
 constexpr int kPackLdsBytes = 33 * 1024;  // keys of one pack tile, [CC][TT + kPackPad]
@@ -523,42 +523,9 @@ __device__ __forceinline__ void stage_and_write(const U* key, const uint32_t* ra
   }
 }
 
-// Pass offsets of a segment with at most kShortMaxTiles pack tiles: one block
-// per (segment, histogram pass), thread d = digit.  binbase[seg][pass][d] =
-// exclusive scan over digits of the segment's digit totals; for pass 0 (the
-// first scatter) also offs[seg][scatter tile][d] = count of digit d in the
-// earlier scatter tiles (2^lm pack tiles each).  Resets the look-back tickets
-// of all npass passes.
+// Segments of at most this many pack tiles sum their tile histograms in the
+// first scatter itself (no offsets kernel).
 constexpr int kShortMaxTiles = 64;
-
-__global__ __launch_bounds__(kSortThreads) void seg_offsets_kernel(
-    const uint16_t* __restrict__ hist, int nt0, int lm, int nh, int npass,
-    uint32_t* __restrict__ offs, int nsct, uint32_t* __restrict__ binbase,
-    uint32_t* __restrict__ tickets, int64_t nseg) {
-  __shared__ uint32_t tmp[kSortThreads / kWave + 1];
-  const int d = threadIdx.x;
-  const int64_t seg = blockIdx.x / nh;
-  const int p = (int)(blockIdx.x - seg * nh);
-  const int per = nh * kRadix;
-  const uint16_t* hs = hist + seg * (int64_t)nt0 * per + p * kRadix + d;
-  uint32_t v[kShortMaxTiles];
-#pragma unroll
-  for (int j = 0; j < kShortMaxTiles; ++j) v[j] = j < nt0 ? hs[(int64_t)j * per] : 0u;
-  uint32_t tot = 0;
-#pragma unroll
-  for (int j = 0; j < kShortMaxTiles; ++j) tot += v[j];
-  binbase[(seg * nh + p) * kRadix + d] = block_excl_scan<kSortThreads>(tot, tmp, nullptr);
-  if (p == 0) {
-    const int mmask = (1 << lm) - 1;
-    uint32_t run = 0;
-#pragma unroll
-    for (int j = 0; j < kShortMaxTiles; ++j) {
-      if (j < nt0 && (j & mmask) == 0) offs[(seg * nsct + (j >> lm)) * kRadix + d] = run;
-      run += v[j];
-    }
-  }
-  if (p == 0 && d < npass) tickets[(int64_t)d * nseg + seg] = 0;  // [pass][seg]
-}
 
 template <typename U, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void scatter0_kernel(
@@ -643,6 +610,61 @@ __device__ __forceinline__ void hist_sums(const uint16_t* __restrict__ hs, int p
   *bef = sb;
   *tot = st;
   __syncthreads();
+}
+
+// The pass-0 scatter of a sort of short segments (at most kShortMaxTiles pack
+// tiles) with its offsets computed in place: each block sums its segment's
+// pack histograms of the low digit before its tile (no offsets kernel); the
+// tile-0 block writes the digit bases of every histogram pass and resets the
+// look-back tickets of the later passes.
+template <typename U, int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void scatter0_offs_kernel(
+    const U* __restrict__ in, U* __restrict__ out, const uint16_t* __restrict__ hist, int nt0,
+    int m, int64_t T, int ntiles, int64_t nblk, int tbits, int nh, int npass,
+    uint32_t* __restrict__ binbase, uint32_t* __restrict__ tickets, int64_t nseg,
+    uint32_t* __restrict__ zero0, int64_t zero0_words) {
+  constexpr int NW = kSortThreads / kWave;
+  constexpr int TILE = kSortThreads * ITEMS;
+  static_assert(TILE * sizeof(U) >= 2 * 8 * kRadix * sizeof(uint16_t), "partial sums in stage");
+  __shared__ uint32_t wcnt[NW][kRadix];
+  __shared__ uint32_t dstart[kRadix];
+  __shared__ int32_t gbase[kRadix];
+  __shared__ uint32_t scan_tmp[NW + 1];
+  __shared__ __align__(16) U stage[TILE];
+  // the rank's peer tables share the staging tile (free until the ranks are done)
+  static_assert(sizeof(U) * TILE >= sizeof(uint64_t) * NW * kRadix, "peer tables fit");
+  uint64_t (*mt)[kRadix] = (uint64_t (*)[kRadix])stage;
+  zero_slice(zero0, zero0_words);  // state of later passes; every block, padding included
+  const int tid = threadIdx.x;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  if (lb >= nblk) return;  // uniform per block
+  const int64_t seg = lb / ntiles;
+  const int tile = (int)(lb - seg * ntiles);
+  const int64_t start = (int64_t)tile * TILE;
+  const int n = (int)((T - start) < TILE ? (T - start) : TILE);
+  const int per = nh * kRadix;
+  const uint16_t* hs = hist + seg * (int64_t)nt0 * per;
+  U key[ITEMS];
+  load_tile<U, ITEMS>(in + seg * T + start, n, key);
+  uint32_t bef, tot;
+  hist_sums<kSortThreads>(hs, per, nt0, tile * m, (uint16_t*)stage, &bef, &tot);
+  const uint32_t base = block_excl_scan<kSortThreads>(tot, scan_tmp, nullptr);
+  if (tile == 0) {
+    binbase[seg * per + tid] = base;
+    for (int p = 1; p < nh; ++p) {  // block-uniform
+      uint32_t b2, t2;
+      hist_sums<kSortThreads>(hs + p * kRadix, per, nt0, 0, (uint16_t*)stage, &b2, &t2);
+      binbase[seg * per + p * kRadix + tid] = block_excl_scan<kSortThreads>(t2, scan_tmp, nullptr);
+    }
+    if (tid < npass) tickets[(int64_t)tid * nseg + seg] = 0;  // [pass][seg]
+  }
+  uint32_t rank[ITEMS];
+  uint32_t own;
+  for (int x = threadIdx.x; x < NW * kRadix; x += kSortThreads) mt[x / kRadix][x % kRadix] = 0;
+  rank_tile<U, ITEMS, kSortThreads, true>(n, tbits, wcnt, dstart, scan_tmp, key, rank, &own, mt);
+  gbase[tid] = (int32_t)((int64_t)bef + (int64_t)base - (int64_t)dstart[tid]);
+  __syncthreads();
+  stage_and_write<U, ITEMS>(key, rank, n, tbits, wcnt, dstart, gbase, stage, out + seg * T, T);
 }
 
 // State of the bucket link's large buckets.  A bucket of more than kLinkPart
@@ -1297,7 +1319,7 @@ int64_t scatter0_tiles(const Tape& tp) {
   return (tp.T + kT - 1) / kT;
 }
 
-// Two 8-bit digits, 32-bit keys, short segments (seg_offsets_kernel): the
+// Two 8-bit digits, 32-bit keys, short segments (at most kShortMaxTiles): the
 // link may go by buckets of the high digit.
 bool bucket_mode(const Tape& tp, size_t key_bytes, int64_t nt0) {
   return key_bytes == 4 && (tp.abits + 7) / 8 == 2 && nt0 <= kShortMaxTiles;
@@ -1387,17 +1409,16 @@ static hipError_t sort_tape_fused(const AddrIn& addr, const uint8_t* wmask,
   if (bucket) {  // bucket_mode() implies nt0 <= kShortMaxTiles and two passes
     scatter0_bucket_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
         ka, kb, hist, nt0, m, tp.T, nsct, nblk0, tp.tbits, binbase, big, tp.nseg());
-  } else if (nt0 <= kShortMaxTiles) {
-    const int lm = __builtin_ctz((unsigned)m);
-    seg_offsets_kernel<<<(unsigned)(tp.nseg() * nh), kSortThreads, 0, s>>>(
-        hist, nt0, lm, nh, npass, offs, nsct, binbase, tickets, tp.nseg());
+  } else if (nt0 <= kShortMaxTiles) {  // the scatter sums the histograms itself
+    scatter0_offs_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
+        ka, kb, hist, nt0, m, tp.T, nsct, nblk0, tp.tbits, nh, npass, binbase, tickets, tp.nseg(),
+        next0, status_words);
   } else {
     scan_hist_kernel<<<(unsigned)tp.nseg(), 1024, 0, s>>>(hist, nt0, m, nh, npass, offs, nsct,
                                                            binbase, tickets);
-  }
-  if (!bucket)
     scatter0_kernel<U, kScatter0Items><<<g0, kSortThreads, 0, s>>>(
         ka, kb, offs, binbase, nh, tp.T, nsct, nblk0, tp.tbits, next0, status_words);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (bucket) {
