@@ -307,6 +307,15 @@ struct Pub<float> {
     *flag = (uint32_t)(w >> 32);
     return *flag != 0;
   }
+  // the words of one value as read once (no wait), and their value when published
+  static __device__ __forceinline__ void peek(uint64_t* p, uint64_t* w) {
+    w[0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  static __device__ __forceinline__ bool decode(const uint64_t* w, float* v, uint32_t* flag) {
+    *v = __uint_as_float((uint32_t)w[0]);
+    *flag = (uint32_t)(w[0] >> 32);
+    return *flag != 0;
+  }
 };
 template <>
 struct Pub<double> {
@@ -324,6 +333,15 @@ struct Pub<double> {
         (long long)(((uint64_t)__float_as_uint(hi) << 32) | (uint64_t)__float_as_uint(lo)));
     *flag = f0;
     return ok;
+  }
+  static __device__ __forceinline__ void peek(uint64_t* p, uint64_t* w) {
+    w[0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    w[1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  static __device__ __forceinline__ bool decode(const uint64_t* w, double* v, uint32_t* flag) {
+    *v = __longlong_as_double((long long)((w[0] << 32) | (w[1] & 0xffffffffull)));
+    *flag = (uint32_t)(w[0] >> 32);
+    return (w[0] >> 32) != 0 && (w[1] >> 32) != 0;
   }
 };
 
@@ -555,16 +573,30 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   for (int cc = 0; cc < kColsPerThread; ++cc) {
     const int col = tid + cc * kWalkThreads;
     if (col < ncol) {
+      // earlier parts newest first, kSumLookBatch words read at once; a part
+      // not yet published is waited for (the order of the additions is fixed)
+      constexpr int kSumLookBatch = 8;
       Acc carry = Acc(0);
-      for (int64_t j = q - 1; j >= 0; --j) {
-        Acc val;
-        uint32_t f;
-        if (!Pub<Acc>::get(status + ((seg * nparts + j) * ncol + col) * PW, &val, &f)) {
-          atomicOr(err, kStatusSumWait);
-          break;
+      bool done = false;
+      for (int64_t j0 = q - 1; j0 >= 0 && !done; j0 -= kSumLookBatch) {
+        uint64_t wv[kSumLookBatch][PW];
+#pragma unroll
+        for (int i = 0; i < kSumLookBatch; ++i)
+          if (j0 - i >= 0) Pub<Acc>::peek(status + ((seg * nparts + j0 - i) * ncol + col) * PW, wv[i]);
+#pragma unroll
+        for (int i = 0; i < kSumLookBatch; ++i) {
+          if (done || j0 - i < 0) break;
+          Acc val;
+          uint32_t f;
+          if (!Pub<Acc>::decode(wv[i], &val, &f) &&
+              !Pub<Acc>::get(status + ((seg * nparts + j0 - i) * ncol + col) * PW, &val, &f)) {
+            atomicOr(err, kStatusSumWait);
+            done = true;
+            break;
+          }
+          carry = val + carry;
+          if (f == 2u) done = true;
         }
-        carry = val + carry;
-        if (f == 2u) break;
       }
       for (int k = 0; k < NW; ++k) {
         const Acc t = tl[k * ncol + col];
