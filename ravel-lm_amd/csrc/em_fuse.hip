@@ -16,8 +16,10 @@
 // fp32 values); wave (g, h) owns rows [64g, 64g+64) and columns
 // [16*CT*h, 16*CT*(h+1)).  A chunk's A tile is gathered in 16-byte units (8
 // 16-bit or 4 fp32 values; P a multiple of that keeps a unit inside one head),
-// W's tile is read row-major, both go to LDS with rows padded to 144 bytes
-// (the 16 rows that one MFMA operand read touches land in distinct banks).  A
+// W's tile is read row-major, both go to LDS with rows padded to 160 bytes
+// (of paddings from 8 to 64 bytes, 32 gave the fewest LDS stalls: 144-byte
+// rows, whose 16 rows of one operand read start on distinct banks, measured
+// 5 % slower).  A
 // wave runs 4 x CT tiles of v_mfma_f32_16x16x32_{bf16,f16} per 32 k, or of four
 // v_mfma_f32_16x16x4_f32 per 16 k (fp32 payloads: lane group g's 16-byte unit
 // holds k = 4g .. 4g+3 and the four MFMAs take one each, the same k order for
@@ -53,7 +55,7 @@ constexpr int kRows = 128;
 constexpr int kSrcLds = 32;  // heads whose sources a block stages in LDS
 constexpr int kCols = 256;   // the widest column tile (CT = 4)
 constexpr int kChunkBytes = 128;  // of one row per K chunk: 8 units of 16 bytes
-constexpr int kLdsBytes = kChunkBytes + 16;  // padded LDS row
+constexpr int kLdsBytes = kChunkBytes + 32;  // padded LDS row (160 B: the fewest LDS stalls measured)
 constexpr int kSets = 2;  // register sets of prefetched chunks (even: LDS parity is static)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
