@@ -10,7 +10,8 @@
 //   out[n, m] = sum_k A[n, k] * W[m, k],   n = b*T + t, k = c*P + p,
 //   A[n, c*P + p] = src[n*C + c] >= 0 ? payload[src[n*C + c]*P + p] : 0.
 //
-// Tiles: a block (8 waves, one block per CU) computes kRows rows x 64*CT
+// Tiles: a block (8 waves; two blocks share a CU at CT = 1, whose registers
+// and LDS allow it, else one) computes kRows rows x 64*CT
 // columns (CT = ceil(M / 64), at most 4; wider M takes more column blocks,
 // grid.y) over K in chunks of 128 bytes of a row (64 bf16/f16 values or 32
 // fp32 values); wave (g, h) owns rows [64g, 64g+64) and columns
@@ -105,7 +106,7 @@ __device__ __forceinline__ void put_out(void* base, int64_t i, float x) {
 __device__ u32x4 kZeroUnit = {0u, 0u, 0u, 0u};  // never written: the unit a missing row reads
 
 template <int DT, bool SRC_LDS, int CT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gather_gemm_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4))) void gather_gemm_kernel(
     const unsigned char* __restrict__ payload, const int32_t* __restrict__ src,
     const unsigned char* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
     unsigned char* __restrict__ out) {
