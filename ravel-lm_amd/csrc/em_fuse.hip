@@ -268,6 +268,168 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4))
   }
 }
 
+// Wide form (16-bit payloads, M > 64, sources staged in LDS): blocks of
+// kWRows = 256 rows, the 8 waves as 4 row groups x 2 column groups, so a wave
+// tile is 64 rows x 16*CW columns (CW up to 8, block columns 32*CW) and every
+// operand fragment read from LDS feeds more MFMAs than in the 64 x 64 tiles
+// above (27 % fewer LDS bytes per flop at M = 256).  K goes in chunks of 64
+// bytes of a row (32 values: one v_mfma_f32_16x16x32 k-step), which keeps the
+// two LDS buffers of both operands and the sources within 128 KB.  The
+// pipeline (two register sets, two LDS buffers, one barrier a chunk, loads
+// without branches) is the one above.
+constexpr int kWRows = 256;
+constexpr int kWChunk = 64;          // bytes of a row per K chunk: 4 units of 16 bytes
+constexpr int kWLds = kWChunk + 32;  // padded LDS row
+constexpr int kWSets = 2;            // register sets of prefetched chunks
+
+template <int DT, int CW>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gather_gemm_wide_kernel(
+    const unsigned char* __restrict__ payload, const int32_t* __restrict__ src,
+    const unsigned char* __restrict__ W, int64_t NR, int C, int P, FastDiv byP, int M, int64_t nsrc,
+    unsigned char* __restrict__ out) {
+  static_assert(DT != kFuseF32, "16-bit payloads");
+  constexpr int ES = 2, VPU = 8;
+  constexpr int KCH = kWChunk / ES;  // k per chunk
+  constexpr int UPR = kWChunk / 16;  // 16-byte units of a row per chunk
+  constexpr int RT = 4;              // 16-row tiles per wave
+  constexpr int BC = 32 * CW;        // columns of the block
+  constexpr int AU = kWRows * UPR / kThreads;
+  constexpr int BUN = BC * UPR;      // W units of a chunk
+  constexpr int BU = (BUN + kThreads - 1) / kThreads;
+  static_assert(AU * kThreads == kWRows * UPR, "whole A units per thread");
+  constexpr int ABYTES = 2 * kWRows * kWLds;
+  constexpr int BBYTES = 2 * BC * kWLds;
+  __shared__ __align__(16) unsigned char lds[ABYTES + BBYTES];
+  __shared__ int32_t Ss[kWRows * kSrcLds];
+  unsigned char* As = lds;
+  unsigned char* Bs = lds + ABYTES;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wrow = wave & 3, wcol = wave >> 2;  // 64-row group, column group
+  const int64_t row0 = (int64_t)blockIdx.x * kWRows;
+  const int col0 = (int)blockIdx.y * BC;
+  const int K = C * P;
+  {
+    const int64_t nrow = (NR - row0) < kWRows ? (NR - row0) : kWRows;
+    for (int i = tid; i < nrow * C; i += kThreads) Ss[i] = src[row0 * C + i];
+    __syncthreads();
+  }
+  f32x4_t acc[RT][CW];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < CW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4 av[kWSets][AU], bv[kWSets][BU];
+  const u32x4* zero = &kZeroUnit;
+  auto load_chunk = [&](int ch, u32x4 (&a)[AU], u32x4 (&bb)[BU]) {
+    const int k0 = ch * KCH;
+#pragma unroll
+    for (int q = 0; q < AU; ++q) {
+      const int u = tid + kThreads * q;
+      const int r = u / UPR, piece = u % UPR;
+      const int k = k0 + piece * VPU;
+      const int64_t n = row0 + r;
+      const bool in = n < NR && k < K;  // a missing or out-of-range unit reads a zero unit
+      const int kc = in ? k : 0;
+      const int c = (int)fdiv((uint32_t)kc, byP);
+      const int32_t sv = Ss[r * C + c];
+      const bool ok = in && sv >= 0 && sv < nsrc;
+      a[q] = *(ok ? (const u32x4*)(payload + ((int64_t)sv * P + (kc - c * P)) * ES) : zero);
+    }
+#pragma unroll
+    for (int q = 0; q < BU; ++q) {
+      const int u = tid + kThreads * q;
+      const int m = col0 + u / UPR, piece = u % UPR;
+      const int k = k0 + piece * VPU;
+      const bool in = u < BUN && m < M && k < K;
+      bb[q] = *(in ? (const u32x4*)(W + ((int64_t)m * K + k) * ES) : zero);
+    }
+  };
+  auto store_chunk = [&](int buf, const u32x4 (&a)[AU], const u32x4 (&bb)[BU]) {
+#pragma unroll
+    for (int q = 0; q < AU; ++q) {
+      const int u = tid + kThreads * q;
+      *(u32x4*)&As[buf * (kWRows * kWLds) + (u / UPR) * kWLds + (u % UPR) * 16] = a[q];
+    }
+#pragma unroll
+    for (int q = 0; q < BU; ++q) {
+      const int u = tid + kThreads * q;
+      if (BU * kThreads == BUN || u < BUN)
+        *(u32x4*)&Bs[buf * (BC * kWLds) + (u / UPR) * kWLds + (u % UPR) * 16] = bb[q];
+    }
+  };
+  auto multiply = [&](int buf) {
+    // one k-step of 32: lane group g holds k = 8g .. 8g + 7 (bytes 16g .. 16g + 15)
+    const int kb = (lane >> 4) * 16;
+    u32x4 b[CW];
+#pragma unroll
+    for (int j = 0; j < CW; ++j)
+      b[j] = *(const u32x4*)&Bs[buf * (BC * kWLds) + (wcol * 16 * CW + j * 16 + (lane & 15)) * kWLds + kb];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const u32x4 a = *(const u32x4*)&As[buf * (kWRows * kWLds) + (wrow * 64 + i * 16 + (lane & 15)) * kWLds + kb];
+#pragma unroll
+      for (int j = 0; j < CW; ++j) acc[i][j] = mfma_unit<DT>(a, b[j], acc[i][j]);
+    }
+  };
+  const int nch = (K + KCH - 1) / KCH;
+  const int nchp = (nch + kWSets - 1) / kWSets * kWSets;
+  auto clampc = [&](int ch) { return ch < nchp ? ch : nchp - 1; };
+#pragma unroll
+  for (int st = 0; st < kWSets; ++st) load_chunk(clampc(st), av[st], bv[st]);
+  store_chunk(0, av[0], bv[0]);
+  __syncthreads();
+  for (int c0 = 0; c0 < nchp; c0 += kWSets) {
+#pragma unroll
+    for (int st = 0; st < kWSets; ++st) {
+      load_chunk(clampc(c0 + st + kWSets), av[st], bv[st]);
+      multiply(st & 1);
+      __builtin_amdgcn_sched_barrier(0);  // the MFMAs issue before the stores wait
+      store_chunk((st + 1) & 1, av[(st + 1) % kWSets], bv[(st + 1) % kWSets]);
+      __syncthreads();
+    }
+  }
+  // Epilogue: one 64-row group at a time staged in LDS (rows of BC + VPU
+  // values), then written in 16-byte units when output rows are whole units.
+  unsigned char* Cs = lds;
+  constexpr int CSTRIDE = BC + VPU;
+  static_assert(64 * CSTRIDE * ES <= ABYTES + BBYTES, "row group fits the buffers");
+  const int ncol = (M - col0) < BC ? (M - col0) : BC;
+  const bool units = (M % VPU) == 0 && ((uintptr_t)out & 15) == 0;
+#pragma unroll 1
+  for (int g = 0; g < 4; ++g) {
+    if (wrow == g) {
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < CW; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = i * 16 + (lane >> 4) * 4 + e;
+            const int col = wcol * 16 * CW + j * 16 + (lane & 15);
+            put_out<DT>(Cs, (int64_t)r * CSTRIDE + col, acc[i][j][e]);
+          }
+    }
+    __syncthreads();
+    if (units) {
+      const int upr = ncol / VPU;
+      for (int u = tid; u < 64 * upr; u += kThreads) {
+        const int r = u / upr, piece = u - (u / upr) * upr;
+        const int64_t n = row0 + g * 64 + r;
+        if (n < NR)
+          *(u32x4*)(out + (n * M + col0 + piece * VPU) * ES) =
+              *(const u32x4*)&Cs[((int64_t)r * CSTRIDE + piece * VPU) * ES];
+      }
+    } else {
+      for (int u = tid; u < 64 * ncol; u += kThreads) {
+        const int r = u / ncol, col = u - (u / ncol) * ncol;
+        const int64_t n = row0 + g * 64 + r;
+        if (n < NR) ((uint16_t*)out)[n * M + col0 + col] = ((const uint16_t*)Cs)[r * CSTRIDE + col];
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, const void* W,
@@ -312,6 +474,32 @@ hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, i
     else
       go(dt, std::false_type{});
   };
+  // 16-bit payloads with M > 64: the wide form (CW 16-column tiles a wave)
+  if ((dtype == kF16 || dtype == kBF16) && M > 64 && C <= kSrcLds) {
+    const int cw = M <= 128 ? 4 : (M <= 192 ? 6 : 8);
+    const int64_t wblocks = (NR + kWRows - 1) / kWRows;
+    const int64_t wncb = (M + 32 * cw - 1) / (32 * cw);
+    if (wblocks > INT32_MAX || wncb > 65535) return hipErrorInvalidValue;
+    const dim3 wgrid((unsigned)wblocks, (unsigned)wncb);
+    auto wide = [&](auto dt) {
+      constexpr int D = decltype(dt)::value;
+#define REM_GW(CW)                                                                           \
+  gather_gemm_wide_kernel<D, CW><<<wgrid, kThreads, 0, s>>>(                                  \
+      (const unsigned char*)payload, src, (const unsigned char*)W, NR, (int)C, (int)P, byP, \
+      (int)M, nsrc, (unsigned char*)out)
+      switch (cw) {
+        case 4: REM_GW(4); break;
+        case 6: REM_GW(6); break;
+        default: REM_GW(8); break;
+      }
+#undef REM_GW
+    };
+    if (dtype == kF16)
+      wide(std::integral_constant<int, kFuseF16>{});
+    else
+      wide(std::integral_constant<int, kFuseBF16>{});
+    return hipGetLastError();
+  }
   if (dtype == kF16)
     by_src(std::integral_constant<int, kFuseF16>{});
   else if (dtype == kF32)
