@@ -13,8 +13,19 @@
  *     ravel_em_last_error() (thread-local).  No C++ exception crosses the ABI.
  *
  * Shapes follow the reference: B batch, T time, C memory heads, A address
- * space, D payload width, k latest-k slots, N = B*T*C records (N < 2^31).
+ * space, D payload width, k latest-k slots, N = B*T*C records.
  * Bool outputs are one byte per element (0/1), matching torch.bool storage.
+ *
+ * Tape sizes.  The reference's int64 key path has no size bound
+ * (ravel_lm/ravel_memory.py:45-49, :159-174).  Here every (b, c) segment holds
+ * records of one batch row, so the entry points that take a [B,T,C] tape
+ * (except ravel_em_sort_order) run a tape whose slots B*T*C*k (records, for
+ * the sums, the prefill and the addresses) pass 2^26 as consecutive ranges of
+ * whole rows of at most 2^26 slots, on the same stream and workspace; their
+ * *_workspace() queries size one range.  What must fit is one batch row:
+ * T*C*k < 2^31.  Outputs that are int32 record indices (out_src, and the
+ * sources that ravel_em_latest_k_bwd takes) need N < 2^31;
+ * ravel_em_sort_order needs N < 2^31.
  */
 #ifndef RAVEL_EM_H
 #define RAVEL_EM_H
@@ -158,6 +169,16 @@ int ravel_em_profile_stop(double* ms, int* calls, int n);
  * so the two can be checked against each other.
  */
 int ravel_em_set_sort_path(int path);
+
+/*
+ * Largest number of slots (records, where a call has no slots) that one row
+ * range of a split call holds, for the calls this thread makes: 0 restores the
+ * default 2^26, and smaller values make calls split at small sizes.  Results
+ * do not depend on it (latest-k, sources, the prefill and addresses bit for
+ * bit; sums within their accumulation bound); the switch exists so the split
+ * can be checked against unsplit calls.  Has no counterpart in the reference.
+ */
+int ravel_em_set_split_slots(int64_t slots);
 
 /*
  * Key width rule of _composite_key_dtype (ravel_lm/ravel_memory.py:45-49):

@@ -87,6 +87,112 @@ int check_tape(int64_t B, int64_t T, int64_t C, int64_t A) {
   return RAVEL_EM_OK;
 }
 
+// ------------------------------------------------------- batch split --
+// Every (b, c) segment holds records of batch row b only, so a tape of B rows
+// is B independent tapes of one row.  A call whose slots (B*T*C*k, or its
+// records where it has no slots) pass kSplitSlots runs as consecutive calls
+// over ranges of whole rows of at most that many slots, on the same stream and
+// the same workspace, which is sized for one range.  This bounds the workspace
+// by the range rather than the tape (a 2^31-slot lookup would otherwise need
+// some 24 GB of keys and sources), keeps the kernels' 32-bit record and slot
+// indices in range however long the tape, and costs the drain of a few
+// kernels per range (under 1 % at 2^26 slots a range).  Inside a range every
+// index is local: the host offsets the rows' pointers and shifts int32 sources
+// by the range's first record.  A range keeps the whole tape's key-width rule
+// (the int32 pass of addresses when the whole tape's composite key is int32),
+// so no record's result depends on the split.  One row must fit a launch:
+// T*C*k < 2^31 (such a row runs as a range of its own).
+constexpr int64_t kSplitSlots = (int64_t)1 << 26;
+
+// Largest slot count of one range; changed only by ravel_em_set_split_slots.
+thread_local int64_t g_split_slots = kSplitSlots;
+
+// Shape check of an entry point that splits its batch.
+int check_rows(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k) {
+  if (B < 0 || T < 0 || C < 0) return fail(RAVEL_EM_EINVAL, "negative shape B=%lld T=%lld C=%lld", (long long)B, (long long)T, (long long)C);
+  if (A < 1) return fail(RAVEL_EM_EINVAL, "address_space must be >= 1, got %lld", (long long)A);
+  if (A > ((int64_t)1 << 40)) return fail(RAVEL_EM_EINVAL, "address_space must be <= 2^40");
+  int64_t tc, row, all;
+  if (!mul_ok(T, C, &tc) || !mul_ok(tc, k, &row) || row > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "T*C*k of one batch row must be < 2^31 (T=%lld C=%lld k=%lld)",
+                (long long)T, (long long)C, (long long)k);
+  if (!mul_ok(B, row, &all)) return fail(RAVEL_EM_EINVAL, "B*T*C*k overflows int64");
+  return RAVEL_EM_OK;
+}
+
+// Rows of one range for per_row slots per batch row (at least one row).
+int64_t split_rows(int64_t B, int64_t per_row) {
+  if (B < 1) return 1;
+  const int64_t r = per_row > 0 ? g_split_slots / per_row : B;
+  return r < 1 ? 1 : (r < B ? r : B);
+}
+
+const void* at(const void* p, int64_t bytes) { return p ? (const char*)p + bytes : nullptr; }
+void* at(void* p, int64_t bytes) { return p ? (char*)p + bytes : nullptr; }
+
+// The address input of the rows from b0 on of a [B, T, C] tape.
+AddrIn addr_rows(const AddrIn& a, int64_t b0, int64_t T, int64_t C) {
+  AddrIn r = a;
+  if (a.kind == kAddrGen) {
+    const int64_t tes = a.gen.tok_dtype == kI64 ? 8 : 4;
+    const int64_t les = a.gen.lg_dtype == kF32 ? 4 : 2;
+    r.gen.tokens = at(a.gen.tokens, b0 * a.gen.tok_sb * tes);
+    r.gen.logits = at(a.gen.logits, b0 * a.gen.lg_sb * les);
+    r.gen.history = at(a.gen.history, b0 * a.gen.hist_sb * tes);
+  } else {
+    r.dense = at(a.dense, b0 * T * C * (a.kind == kI64 ? 8 : 4));
+  }
+  return r;
+}
+
+// Status words of a split call, after each range: word kStatusSplitWord
+// collects the ranges' bits, and the last range's word 0 receives them all.
+__global__ void status_fold_kernel(uint32_t* __restrict__ hdr, int first, int last) {
+  if (threadIdx.x == 0) {
+    const uint32_t acc = hdr[0] | (first ? 0u : hdr[kStatusSplitWord]);
+    hdr[kStatusSplitWord] = acc;
+    if (last) hdr[0] = acc;
+  }
+}
+
+// out[i] = in[i] + delta where 0 <= in[i] + delta < limit, else -1 (in place
+// allowed): range-local sources to the whole tape's and back.
+__global__ __launch_bounds__(256) void shift_sources_kernel(const int32_t* in, int64_t n,
+                                                           int64_t delta, int64_t limit,
+                                                           int32_t* out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = in[i];
+    const int64_t w = v + delta;
+    out[i] = v >= 0 && w >= 0 && w < limit ? (int32_t)w : -1;
+  }
+}
+
+hipError_t shift_sources(const int32_t* in, int64_t n, int64_t delta, int64_t limit, int32_t* out,
+                         hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  shift_sources_kernel<<<grid_for(n, 256), 256, 0, s>>>(in, n, delta, limit, out);
+  return hipGetLastError();
+}
+
+// Runs fn(rows, b0) over consecutive ranges of at most `rows` batch rows; a
+// workspace that holds a status header gets its words folded after each range.
+template <class F>
+int split_batch(int64_t B, int64_t rows, void* ws, size_t wsb, hipStream_t s, F&& fn) {
+  if (rows >= B) return fn(B, (int64_t)0);
+  const bool hdr = ws && wsb >= kStatusBytes;
+  for (int64_t b0 = 0; b0 < B; b0 += rows) {
+    const int64_t nb = rows < B - b0 ? rows : B - b0;
+    if (int rc = fn(nb, b0)) return rc;
+    if (hdr) {
+      status_fold_kernel<<<1, 64, 0, s>>>((uint32_t*)ws, b0 == 0, b0 + nb >= B);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return hip_fail(e, "status word");
+    }
+  }
+  return RAVEL_EM_OK;
+}
+
 int check_addr_dtype(int dt, bool gen_ok = true) {
   if (dt == kAddrGen && gen_ok) return RAVEL_EM_OK;
   if (dt != kI32 && dt != kI64)
@@ -333,6 +439,19 @@ int resolve_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   return RAVEL_EM_OK;
 }
 
+// The resolve of rows [b0, b0 + nb) of a tape: range-local sources into src.
+int resolve_rows(const AddrPair& ap, const uint8_t* write_mask, const Tape& tp, int64_t nb,
+                 int64_t b0, int64_t k, int32_t* src, void* ws, size_t wsb, hipStream_t s) {
+  Tape t = tp;
+  t.B = nb;
+  const AddrIn w = addr_rows(ap.w, b0, tp.T, tp.C);
+  AddrIn r;
+  if (ap.rp) r = addr_rows(*ap.rp, b0, tp.T, tp.C);
+  const uint8_t* wm = write_mask ? write_mask + b0 * tp.T : nullptr;
+  return t.wide() ? resolve_run<uint64_t>(w, ap.rp ? &r : nullptr, wm, t, k, src, ws, wsb, s)
+                  : resolve_run<uint32_t>(w, ap.rp ? &r : nullptr, wm, t, k, src, ws, wsb, s);
+}
+
 template <typename U>
 size_t latest_k_ws_t(const Tape& tp, int64_t k, bool link, bool want_src) {
   Bump bp(nullptr);
@@ -533,6 +652,27 @@ int latest_k_bwd_sorted(const int32_t* src, const void* grad_values, int dtype, 
   return RAVEL_EM_OK;
 }
 
+
+// Workspace of the sorted backward: the sort and sums of one range of rows,
+// then (when the batch splits) the range's sources made range-local.
+struct BwdSplit {
+  int64_t rows;
+  size_t local_off;
+  size_t bytes;
+};
+
+BwdSplit bwd_split_plan(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k, int dtype) {
+  BwdSplit p;
+  p.rows = split_rows(B, T * C * k);
+  const int64_t n = (B < p.rows ? B : p.rows) * T * C;
+  const Tape tp = bwd_tape(n, k);
+  const size_t run = tp.wide() ? sum_ws_t<uint64_t>(tp, D, dtype, true, false)
+                               : sum_ws_t<uint32_t>(tp, D, dtype, true, false);
+  p.local_off = (run + 255) / 256 * 256;
+  p.bytes = p.rows < B ? p.local_off + (size_t)(n * k) * sizeof(int32_t) : run;
+  if (p.rows >= B) p.local_off = run;
+  return p;
+}
 }  // namespace
 
 void stage_begin(int stage, hipStream_t s) {
@@ -625,7 +765,7 @@ int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64
   g_err.clear();
   if (!gen) return fail(RAVEL_EM_EINVAL, "null pointer");
   const int64_t C = (int64_t)gen->n_literal + gen->n_learned;
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (out_dtype != kI32 && out_dtype != kI64)
     return fail(RAVEL_EM_EINVAL, "address output must be int32 or int64 (code %d)", out_dtype);
   if (out_dtype == kI32 && A > INT32_MAX)
@@ -635,15 +775,31 @@ int ravel_em_addresses(const ravel_em_addr_gen* gen, int64_t B, int64_t T, int64
   const Tape tp = make_tape(B, T, C, A, false, kWrap);
   if (tp.n() == 0) return RAVEL_EM_OK;
   if (!out) return fail(RAVEL_EM_EINVAL, "null pointer");
-  hipError_t e = write_addresses(a, tp, out_dtype, out, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "addresses");
-  return RAVEL_EM_OK;
+  const int64_t es = out_dtype == kI64 ? 8 : 4;
+  return split_batch(B, split_rows(B, T * C), nullptr, 0, (hipStream_t)stream,
+                     [&](int64_t nb, int64_t b0) -> int {
+    Tape t = tp;
+    t.B = nb;
+    hipError_t e = write_addresses(addr_rows(a, b0, T, C), t, out_dtype,
+                                   at(out, b0 * T * C * es), (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "addresses");
+    return RAVEL_EM_OK;
+  });
 }
 
 int ravel_em_set_sort_path(int path) {
   g_err.clear();
   if (path != 0 && path != 1) return fail(RAVEL_EM_EINVAL, "sort path must be 0 (automatic) or 1 (generic)");
   g_sort_path = path;
+  return RAVEL_EM_OK;
+}
+
+int ravel_em_set_split_slots(int64_t slots) {
+  g_err.clear();
+  if (slots < 0 || slots > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "split slots must be in [1, 2^31-1] (0 = the default 2^26), got %lld",
+                (long long)slots);
+  g_split_slots = slots == 0 ? kSplitSlots : slots;
   return RAVEL_EM_OK;
 }
 
@@ -725,8 +881,9 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
 
 size_t ravel_em_latest_k_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
                                    int has_read, int has_mask, int want_src) {
-  if (check_tape(B, T, C, A) || k < 1) return 0;
-  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  if (k < 1 || check_rows(B, T, C, A, k)) return 0;
+  const int64_t rows = split_rows(B, T * C * k);
+  const Tape tp = make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kWrap);
   const bool link = !has_read && !has_mask;
   return tp.wide() ? latest_k_ws_t<uint64_t>(tp, k, link, want_src != 0)
                    : latest_k_ws_t<uint32_t>(tp, k, link, want_src != 0);
@@ -738,14 +895,14 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
                           void* out_values, uint8_t* out_mask, int32_t* out_src, void* workspace,
                           size_t workspace_bytes, void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  if (int rc = check_rows(B, T, C, A, k)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
-  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
   if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
-  int64_t nk;
-  if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
-    return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
+  if (out_src && B * T * C > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "int32 sources need B*T*C < 2^31 (out_src = NULL gives values "
+                                 "and mask of any tape)");
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !out_values || !out_mask) return fail(RAVEL_EM_EINVAL, "null pointer");
@@ -753,11 +910,29 @@ int ravel_em_latest_k_fwd(const void* write_addr, const void* read_addr, int add
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   const int64_t row_bytes = D * dtype_size(payload_dtype);
   hipStream_t s = (hipStream_t)stream;
-  if (tp.wide())
-    return latest_k_run<uint64_t>(ap.w, ap.rp, write_mask, payload, row_bytes, tp, k, out_values,
-                                  out_mask, out_src, workspace, workspace_bytes, s);
-  return latest_k_run<uint32_t>(ap.w, ap.rp, write_mask, payload, row_bytes, tp, k, out_values,
-                                out_mask, out_src, workspace, workspace_bytes, s);
+  const int64_t rows = split_rows(B, T * C * k);
+  return split_batch(B, rows, workspace, workspace_bytes, s, [&](int64_t nb, int64_t b0) -> int {
+    Tape t = tp;
+    t.B = nb;
+    const int64_t r0 = b0 * T * C;  // first record of the range
+    const AddrIn w = addr_rows(ap.w, b0, T, C);
+    AddrIn r;
+    if (ap.rp) r = addr_rows(*ap.rp, b0, T, C);
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    const void* pl = at(payload, r0 * row_bytes);
+    void* ov = at(out_values, r0 * k * row_bytes);
+    uint8_t* om = out_mask + r0 * k;
+    int32_t* os = out_src ? out_src + r0 * k : nullptr;
+    int rc = t.wide() ? latest_k_run<uint64_t>(w, ap.rp ? &r : nullptr, wm, pl, row_bytes, t, k,
+                                               ov, om, os, workspace, workspace_bytes, s)
+                      : latest_k_run<uint32_t>(w, ap.rp ? &r : nullptr, wm, pl, row_bytes, t, k,
+                                               ov, om, os, workspace, workspace_bytes, s);
+    if (rc == RAVEL_EM_OK && os && b0 > 0) {
+      const hipError_t e = shift_sources(os, t.n() * k, r0, B * T * C, os, s);
+      if (e != hipSuccess) return hip_fail(e, "sources");
+    }
+    return rc;
+  });
 }
 
 int ravel_em_latest_k_fwd_static(const void* write_addr, const void* read_addr, int addr_dtype,
@@ -766,8 +941,8 @@ int ravel_em_latest_k_fwd_static(const void* write_addr, const void* read_addr, 
                                  int64_t A, int64_t k, void* out_values, uint8_t* out_mask,
                                  int32_t* out_src, uint32_t* out_status, void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
   if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  if (int rc = check_rows(B, T, C, A, k)) return rc;
   const size_t need = ravel_em_latest_k_workspace(B, T, C, A, k, read_addr != nullptr,
                                                   write_mask != nullptr, out_src != nullptr);
   if (need > kStaticScratchBytes)
@@ -789,43 +964,51 @@ int ravel_em_latest_k_fwd_static(const void* write_addr, const void* read_addr, 
 
 size_t ravel_em_latest_k_resolve_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,
                                            int has_read, int has_mask) {
-  if (check_tape(B, T, C, A) || k < 1) return 0;
-  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  if (k < 1 || check_tape(B, T, C, A) || check_rows(B, T, C, A, k)) return 0;
+  const int64_t rows = split_rows(B, T * C * k);
+  const Tape tp = make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kWrap);
   Bump bp(nullptr);
   bp.off = sort_bytes(tp);
   if (!has_read && !has_mask && C > 1) bp.take<int32_t>((size_t)(tp.n() * k));
   return bp.off;
 }
 
+
 int ravel_em_latest_k_resolve(const void* write_addr, const void* read_addr, int addr_dtype,
                               const uint8_t* write_mask, int64_t B, int64_t T, int64_t C,
                               int64_t A, int64_t k, int32_t* out_src, void* workspace,
                               size_t workspace_bytes, void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_tape(B, T, C, A)) return rc;  // int32 sources: N < 2^31
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
   if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
-  int64_t nk;
-  if (!mul_ok(B * T * C, k, &nk) || nk > kMaxRecords)
-    return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
+  if (int rc = check_rows(B, T, C, A, k)) return rc;
   const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
   if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !out_src) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if (tp.wide())
-    return resolve_run<uint64_t>(ap.w, ap.rp, write_mask, tp, k, out_src, workspace,
-                                 workspace_bytes, s);
-  return resolve_run<uint32_t>(ap.w, ap.rp, write_mask, tp, k, out_src, workspace,
-                               workspace_bytes, s);
+  const int64_t rows = split_rows(B, T * C * k);
+  return split_batch(B, rows, workspace, workspace_bytes, s, [&](int64_t nb, int64_t b0) -> int {
+    const int64_t r0 = b0 * T * C;
+    int32_t* os = out_src + r0 * k;
+    int rc = resolve_rows(ap, write_mask, tp, nb, b0, k, os, workspace, workspace_bytes, s);
+    if (rc == RAVEL_EM_OK && b0 > 0) {
+      const hipError_t e = shift_sources(os, nb * T * C * k, r0, tp.n(), os, s);
+      if (e != hipSuccess) return hip_fail(e, "sources");
+    }
+    return rc;
+  });
 }
 
 size_t ravel_em_latest1_linear_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
                                          int has_read, int want_src) {
-  if (check_tape(B, T, C, A)) return 0;
-  size_t bytes = ravel_em_latest_k_resolve_workspace(B, T, C, A, 1, has_read, 0);
-  if (!want_src) bytes = (bytes + 255) / 256 * 256 + (size_t)(B * T * C) * sizeof(int32_t);
+  if (check_rows(B, T, C, A, 1)) return 0;
+  const int64_t rows = split_rows(B, T * C);
+  const int64_t nb = B < rows ? B : rows;
+  size_t bytes = ravel_em_latest_k_resolve_workspace(nb, T, C, A, 1, has_read, 0);
+  if (!want_src) bytes = (bytes + 255) / 256 * 256 + (size_t)(nb * T * C) * sizeof(int32_t);
   return bytes;
 }
 
@@ -835,7 +1018,7 @@ int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, i
                                 void* out, int32_t* out_src, void* workspace,
                                 size_t workspace_bytes, void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
   if (payload_dtype != kBF16 && payload_dtype != kF16 && payload_dtype != kF32)
     return fail(RAVEL_EM_EINVAL,
@@ -846,29 +1029,46 @@ int ravel_em_latest1_linear_fwd(const void* write_addr, const void* read_addr, i
                 "the fused latest-1 linear needs P %% 8 == 0 (16-bit payloads) or P %% 4 == 0 "
                 "(f32) and 16-byte aligned payload and weight (P=%lld M=%lld)",
                 (long long)P, (long long)M);
+  if (out_src && B * T * C > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "int32 sources need B*T*C < 2^31 (out_src = NULL gives the "
+                                 "output of any tape)");
   if (B * T * C == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !payload || !weight || !out) return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
+  const Tape tp = make_tape(B, T, C, A, false, kWrap);
+  const int64_t rows = split_rows(B, T * C);
+  const int64_t nbmax = B < rows ? B : rows;
   // Sources: into out_src when given, else at the end of the workspace.
-  const size_t rws = ravel_em_latest_k_resolve_workspace(B, T, C, A, 1, read_addr != nullptr, 0);
-  int32_t* src = out_src;
-  if (!src) {
+  const size_t rws = ravel_em_latest_k_resolve_workspace(nbmax, T, C, A, 1, read_addr != nullptr, 0);
+  int32_t* src_ws = nullptr;
+  if (!out_src) {
     const size_t off = (rws + 255) / 256 * 256;
-    if (workspace_bytes < off + (size_t)(B * T * C) * sizeof(int32_t))
+    if (workspace_bytes < off + (size_t)(nbmax * T * C) * sizeof(int32_t))
       return fail(RAVEL_EM_EWORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes,
-                  off + (size_t)(B * T * C) * sizeof(int32_t));
-    src = (int32_t*)((char*)workspace + off);
+                  off + (size_t)(nbmax * T * C) * sizeof(int32_t));
+    src_ws = (int32_t*)((char*)workspace + off);
   }
   hipStream_t s = (hipStream_t)stream;
-  stage_begin(kStageResolve, s);
-  int rc = ravel_em_latest_k_resolve(write_addr, read_addr, addr_dtype, nullptr, B, T, C, A, 1, src,
-                                     workspace, workspace_bytes, stream);
-  stage_end(kStageResolve, s);
-  if (rc != RAVEL_EM_OK) return rc;
-  stage_begin(kStageGather, s);
-  hipError_t e = gather_gemm(payload, src, weight, payload_dtype, B * T, C, P, M, out, s);
-  stage_end(kStageGather, s);
-  if (e != hipSuccess) return hip_fail(e, "gather-GEMM");
-  return RAVEL_EM_OK;
+  const int64_t es = dtype_size(payload_dtype);
+  return split_batch(B, rows, workspace, workspace_bytes, s, [&](int64_t nb, int64_t b0) -> int {
+    const int64_t r0 = b0 * T * C;
+    int32_t* src = out_src ? out_src + r0 : src_ws;
+    stage_begin(kStageResolve, s);
+    int rc = resolve_rows(ap, nullptr, tp, nb, b0, 1, src, workspace, workspace_bytes, s);
+    stage_end(kStageResolve, s);
+    if (rc != RAVEL_EM_OK) return rc;
+    stage_begin(kStageGather, s);
+    hipError_t e = gather_gemm(at(payload, r0 * P * es), src, weight, payload_dtype, nb * T, C, P,
+                               M, at(out, b0 * T * M * es), s);
+    stage_end(kStageGather, s);
+    if (e != hipSuccess) return hip_fail(e, "gather-GEMM");
+    if (out_src && b0 > 0) {
+      e = shift_sources(src, nb * T * C, r0, tp.n(), src, s);
+      if (e != hipSuccess) return hip_fail(e, "sources");
+    }
+    return RAVEL_EM_OK;
+  });
 }
 
 int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, const int32_t* src,
@@ -877,28 +1077,28 @@ int ravel_em_gather_rows(const void* rows, int64_t n_src, int64_t row_bytes, con
   if (n_src < 0 || n_rows < 0 || row_bytes < 1)
     return fail(RAVEL_EM_EINVAL, "bad gather sizes n_src=%lld n_rows=%lld row_bytes=%lld",
                 (long long)n_src, (long long)n_rows, (long long)row_bytes);
-  if (n_src > kMaxRecords || n_rows > kMaxRecords) return fail(RAVEL_EM_EINVAL, "row counts must be < 2^31");
+  if (n_src > kMaxRecords) return fail(RAVEL_EM_EINVAL, "int32 sources address < 2^31 rows");
   if (n_rows == 0) return RAVEL_EM_OK;
   if ((n_src > 0 && !rows) || !src || !out_values) return fail(RAVEL_EM_EINVAL, "null pointer");
-  hipError_t e = gather_rows(rows, n_src, src, n_rows, row_bytes, out_values, out_mask,
-                             (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "gather");
+  // output rows in ranges of at most g_split_slots (each row is independent)
+  for (int64_t i0 = 0; i0 < n_rows; i0 += g_split_slots) {
+    const int64_t n = n_rows - i0 < g_split_slots ? n_rows - i0 : g_split_slots;
+    hipError_t e = gather_rows(rows, n_src, src + i0, n, row_bytes, at(out_values, i0 * row_bytes),
+                               out_mask ? out_mask + i0 : nullptr, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "gather");
+  }
   return RAVEL_EM_OK;
 }
 
 size_t ravel_em_latest_k_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t k,
                                        int payload_dtype, int chain) {
-  if (check_tape(B, T, C, 1) || k < 1 || D < 1) return 0;
-  const int64_t N = B * T * C;
+  if (k < 1 || D < 1 || check_tape(B, T, C, 1) || check_rows(B, T, C, 1, k)) return 0;
   if (chain) {
     Bump bp(nullptr);
-    bp.take<int32_t>((size_t)N);
+    bp.take<int32_t>((size_t)(B * T * C));
     return bp.off;
   }
-  if (N * k > kMaxRecords) return 0;
-  const Tape tp = bwd_tape(N, k);
-  return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, true, false)
-                   : sum_ws_t<uint32_t>(tp, D, payload_dtype, true, false);
+  return bwd_split_plan(B, T, C, D, k, payload_dtype).bytes;
 }
 
 int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int payload_dtype,
@@ -906,9 +1106,10 @@ int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int paylo
                           void* grad_payload, void* workspace, size_t workspace_bytes,
                           void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, 1)) return rc;
+  if (int rc = check_tape(B, T, C, 1)) return rc;  // int32 sources: N < 2^31
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (k < 1 || D < 1) return fail(RAVEL_EM_EINVAL, "k and D must be positive");
+  if (int rc = check_rows(B, T, C, 1, k)) return rc;
   const int64_t N = B * T * C;
   if (N == 0) return chain ? RAVEL_EM_OK : clear_status(workspace, workspace_bytes, stream);
   if (!src || !grad_values || !grad_payload) return fail(RAVEL_EM_EINVAL, "null pointer");
@@ -922,18 +1123,35 @@ int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int paylo
     if (e != hipSuccess) return hip_fail(e, "latest-k backward");
     return RAVEL_EM_OK;
   }
-  if (N * k > kMaxRecords) return fail(RAVEL_EM_EINVAL, "B*T*C*k must be < 2^31");
-  return bwd_tape(N, k).wide()
-             ? latest_k_bwd_sorted<uint64_t>(src, grad_values, payload_dtype, N, D, k,
-                                             grad_payload, workspace, workspace_bytes, s)
-             : latest_k_bwd_sorted<uint32_t>(src, grad_values, payload_dtype, N, D, k,
-                                             grad_payload, workspace, workspace_bytes, s);
+  const BwdSplit plan = bwd_split_plan(B, T, C, D, k, payload_dtype);
+  if (workspace_bytes < plan.bytes)
+    return fail(RAVEL_EM_EWORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, plan.bytes);
+  const int64_t es = dtype_size(payload_dtype);
+  return split_batch(B, plan.rows, workspace, workspace_bytes, s, [&](int64_t nb, int64_t b0) -> int {
+    const int64_t r0 = b0 * T * C;
+    const int64_t n = nb * T * C;
+    const int32_t* sr = src + r0 * k;
+    if (plan.rows < B) {  // range-local source ids, others dropped
+      int32_t* local = (int32_t*)((char*)workspace + plan.local_off);
+      const hipError_t e = shift_sources(sr, n * k, -r0, n, local, s);
+      if (e != hipSuccess) return hip_fail(e, "latest-k backward");
+      sr = local;
+    }
+    const void* gv = at(grad_values, r0 * k * D * es);
+    void* gp = at(grad_payload, r0 * D * es);
+    return bwd_tape(n, k).wide()
+               ? latest_k_bwd_sorted<uint64_t>(sr, gv, payload_dtype, n, D, k, gp, workspace,
+                                               plan.local_off, s)
+               : latest_k_bwd_sorted<uint32_t>(sr, gv, payload_dtype, n, D, k, gp, workspace,
+                                               plan.local_off, s);
+  });
 }
 
 size_t ravel_em_seg_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
                                   int has_read, int has_mask, int payload_dtype) {
-  if (check_tape(B, T, C, A) || D < 1) return 0;
-  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  if (check_rows(B, T, C, A, 1) || D < 1) return 0;
+  const int64_t rows = split_rows(B, T * C);
+  const Tape tp = make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kWrap);
   const bool direct = !has_read && !has_mask;
   return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, direct, false)
                    : sum_ws_t<uint32_t>(tp, D, payload_dtype, direct, false);
@@ -945,7 +1163,7 @@ int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr
                          uint8_t* out_mask, void* workspace, size_t workspace_bytes,
                          void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
@@ -955,17 +1173,32 @@ int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if (tp.wide())
-    return seg_sum_run<uint64_t>(ap.w, ap.rp, write_mask, payload, payload_dtype, tp, D, out_sum,
-                                 out_mask, workspace, workspace_bytes, s);
-  return seg_sum_run<uint32_t>(ap.w, ap.rp, write_mask, payload, payload_dtype, tp, D, out_sum,
-                               out_mask, workspace, workspace_bytes, s);
+  const int64_t row_bytes = D * dtype_size(payload_dtype);
+  return split_batch(B, split_rows(B, T * C), workspace, workspace_bytes, s,
+                     [&](int64_t nb, int64_t b0) -> int {
+    Tape t = tp;
+    t.B = nb;
+    const int64_t r0 = b0 * T * C;
+    const AddrIn w = addr_rows(ap.w, b0, T, C);
+    AddrIn r;
+    if (ap.rp) r = addr_rows(*ap.rp, b0, T, C);
+    const AddrIn* rp = ap.rp ? &r : nullptr;
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    const void* pl = at(payload, r0 * row_bytes);
+    void* os = at(out_sum, r0 * row_bytes);
+    uint8_t* om = out_mask + r0;
+    return t.wide() ? seg_sum_run<uint64_t>(w, rp, wm, pl, payload_dtype, t, D, os, om, workspace,
+                                            workspace_bytes, s)
+                    : seg_sum_run<uint32_t>(w, rp, wm, pl, payload_dtype, t, D, os, om, workspace,
+                                            workspace_bytes, s);
+  });
 }
 
 size_t ravel_em_seg_sum_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
                                       int has_read, int has_mask, int payload_dtype) {
-  if (check_tape(B, T, C, A) || D < 1) return 0;
-  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  if (check_rows(B, T, C, A, 1) || D < 1) return 0;
+  const int64_t rows = split_rows(B, T * C);
+  const Tape tp = make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kWrap);
   const bool direct = !has_read && !has_mask;
   return tp.wide() ? sum_ws_t<uint64_t>(tp, D, payload_dtype, direct, true)
                    : sum_ws_t<uint32_t>(tp, D, payload_dtype, direct, true);
@@ -977,7 +1210,7 @@ int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr
                          void* grad_payload, void* workspace, size_t workspace_bytes,
                          void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
   if (int rc = check_payload_dtype(payload_dtype)) return rc;
   if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
@@ -987,11 +1220,24 @@ int ravel_em_seg_sum_bwd(const void* write_addr, const void* read_addr, int addr
   AddrPair ap;
   if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
   hipStream_t s = (hipStream_t)stream;
-  if (tp.wide())
-    return seg_sum_bwd_run<uint64_t>(ap.w, ap.rp, write_mask, grad_sum, payload_dtype, tp, D,
-                                     grad_payload, workspace, workspace_bytes, s);
-  return seg_sum_bwd_run<uint32_t>(ap.w, ap.rp, write_mask, grad_sum, payload_dtype, tp, D,
-                                   grad_payload, workspace, workspace_bytes, s);
+  const int64_t row_bytes = D * dtype_size(payload_dtype);
+  return split_batch(B, split_rows(B, T * C), workspace, workspace_bytes, s,
+                     [&](int64_t nb, int64_t b0) -> int {
+    Tape t = tp;
+    t.B = nb;
+    const int64_t r0 = b0 * T * C;
+    const AddrIn w = addr_rows(ap.w, b0, T, C);
+    AddrIn r;
+    if (ap.rp) r = addr_rows(*ap.rp, b0, T, C);
+    const AddrIn* rp = ap.rp ? &r : nullptr;
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    const void* g = at(grad_sum, r0 * row_bytes);
+    void* gp = at(grad_payload, r0 * row_bytes);
+    return t.wide() ? seg_sum_bwd_run<uint64_t>(w, rp, wm, g, payload_dtype, t, D, gp, workspace,
+                                                workspace_bytes, s)
+                    : seg_sum_bwd_run<uint32_t>(w, rp, wm, g, payload_dtype, t, D, gp, workspace,
+                                                workspace_bytes, s);
+  });
 }
 
 static int check_cache(int addr_dtype, int payload_dtype, int64_t B, int64_t C, int64_t A,
@@ -1057,8 +1303,9 @@ int ravel_em_cache_step(void* values, uint8_t* filled, const void* read_addr,
 
 size_t ravel_em_cache_prefill_workspace(int64_t B, int64_t T, int64_t C, int64_t A,
                                         int has_mask) {
-  if (check_tape(B, T, C, A)) return 0;
-  return sort_bytes(make_tape(B, T, C, A, has_mask != 0, kClamp));
+  if (check_rows(B, T, C, A, 1)) return 0;
+  const int64_t rows = split_rows(B, T * C);
+  return sort_bytes(make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kClamp));
 }
 
 int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t* write_mask,
@@ -1067,7 +1314,7 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
                            uint8_t* filled, void* workspace, size_t workspace_bytes,
                            void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D, true)) return rc;
   if (B * C == 0) return RAVEL_EM_OK;
   if (!values || !filled || (B * T * C > 0 && (!write_addr || !payload)))
@@ -1075,28 +1322,39 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
   AddrIn wa;
   if (B * T * C > 0)
     if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
-  Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
+  const Tape full = make_tape(B, T, C, A, write_mask != nullptr, kClamp);
   hipStream_t s = (hipStream_t)stream;
   const int64_t row_bytes = D * dtype_size(payload_dtype);
-  auto run = [&](auto tag) -> int {
-    using U = decltype(tag);
-    Bump bp(workspace);
-    SortWs<U> sw = take_sort<U>(bp, tp);
-    tp.status = sw.status;
-    if (int rc = check_ws(bp, workspace_bytes)) return rc;
-    U* sorted = nullptr;
-    hipError_t e = hipSuccess;
-    if (tp.n() > 0) {
-      e = sort_call<U>(wa, write_mask, tp, sw, &sorted, s);
-      if (e != hipSuccess) return hip_fail(e, "sort");
-    } else if (int rc = clear_status(workspace, workspace_bytes, stream)) {
-      return rc;
-    }
-    e = cache_prefill<U>(sorted, payload, tp, k, row_bytes, values, filled, s);
-    if (e != hipSuccess) return hip_fail(e, "cache prefill");
-    return RAVEL_EM_OK;
-  };
-  return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+  const int64_t slots_per_row = C * A * k;  // cache slots of one stream
+  return split_batch(B, split_rows(B, T * C), workspace, workspace_bytes, s,
+                     [&](int64_t nb, int64_t b0) -> int {
+    Tape tp = full;
+    tp.B = nb;
+    const AddrIn w = B * T * C > 0 ? addr_rows(wa, b0, T, C) : wa;
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    const void* pl = at(payload, b0 * T * C * row_bytes);
+    void* vals = at(values, b0 * slots_per_row * row_bytes);
+    uint8_t* fl = filled + b0 * slots_per_row;
+    auto run = [&](auto tag) -> int {
+      using U = decltype(tag);
+      Bump bp(workspace);
+      SortWs<U> sw = take_sort<U>(bp, tp);
+      tp.status = sw.status;
+      if (int rc = check_ws(bp, workspace_bytes)) return rc;
+      U* sorted = nullptr;
+      hipError_t e = hipSuccess;
+      if (tp.n() > 0) {
+        e = sort_call<U>(w, wm, tp, sw, &sorted, s);
+        if (e != hipSuccess) return hip_fail(e, "sort");
+      } else if (int rc = clear_status(workspace, workspace_bytes, stream)) {
+        return rc;
+      }
+      e = cache_prefill<U>(sorted, pl, tp, k, row_bytes, vals, fl, s);
+      if (e != hipSuccess) return hip_fail(e, "cache prefill");
+      return RAVEL_EM_OK;
+    };
+    return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+  });
 }
 
 }  // extern "C"

@@ -25,8 +25,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Address reduction modes: the lookups wrap with Python remainder
 // (ravel_memory.py:127-128), the decode cache clamps (ravel_memory.py:276,289).
-// kNegLast sorts values already in [0, A) as they are and negative ones at the
-// sentinel A, last (the backward's sort of source record ids, -1 = none).
+// kNegLast sorts values already in [0, A) as they are and any other (-1 =
+// none) at the sentinel A, last (the backward's sort of source record ids).
 enum AddrMode : int { kWrap = 0, kClamp = 1, kNegLast = 2 };
 
 // Host-side description of one event tape.
@@ -81,6 +81,9 @@ struct AddrIn {
 constexpr uint32_t kStatusSortWait = 1u;  // a sort pass's tile look-back
 constexpr uint32_t kStatusSumWait = 2u;   // the segmented sum's part look-back
 constexpr size_t kStatusBytes = 256;
+// word 1: the bits of the earlier row ranges of a call split by batch rows
+// (each range's first kernel clears word 0)
+constexpr int kStatusSplitWord = 1;
 // words 2-3 of the status area: the merged sum kernel's start gate (a
 // launch sequence number and a count; a scheduling hint, never an error)
 constexpr int kStatusGateWord = 2;
@@ -170,7 +173,7 @@ __device__ __forceinline__ uint32_t count_below(uint64_t mask) {
 
 __device__ __forceinline__ int64_t reduce_addr(int64_t a, int64_t A, int mode, bool trunc32) {
   if (mode == kClamp) return a < 0 ? 0 : (a >= A ? A - 1 : a);
-  if (mode == kNegLast) return a < 0 ? A : a;
+  if (mode == kNegLast) return (uint64_t)a < (uint64_t)A ? a : A;
   if (trunc32) a = (int64_t)(int32_t)(uint32_t)(uint64_t)a;
   if ((uint64_t)a < (uint64_t)A) return a;
   const int64_t r = a % A;

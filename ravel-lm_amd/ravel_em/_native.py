@@ -53,6 +53,7 @@ SIGNATURES = {
     "ravel_em_addresses": (_i, [_vp, _i64, _i64, _i64, _i, _vp, _vp]),
     "ravel_em_key_bits": (_i, [_i64, _i64, _i64, _i64]),
     "ravel_em_set_sort_path": (_i, [_i]),
+    "ravel_em_set_split_slots": (_i, [_i64]),
     "ravel_em_profile_start": (_i, []),
     "ravel_em_profile_stop": (_i, [_vp, _vp, _i]),
     "ravel_em_sort_order_workspace": (_sz, [_i64, _i64, _i64, _i64, _i]),

@@ -131,8 +131,30 @@ def test_invalid_arguments_rejected_without_launch():
     rc = lib.ravel_em_seg_sum_fwd(None, None, nat.INT64, None, None, 99,
                                   2, 3, 4, 5, 7, None, None, None, 0, None)
     assert rc == 1 and "payload dtype" in _err()
+    # one batch row must fit the kernels' 32-bit indices ...
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   2, 1 << 27, 1 << 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "one batch row" in _err()
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   2, 1 << 26, 1 << 4, 5, 7, 2, None, None, None, None, 0, None)
+    assert rc == 1 and "one batch row" in _err()
+    # ... while a tape of many rows past 2^31 slots is accepted (split by rows)
     rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
                                    1 << 20, 1 << 12, 1 << 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 1 and "null" in _err()
+    # int32 sources of such a tape do not exist
+    fake = ctypes.c_void_p(0x1000)
+    rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                   1 << 20, 1 << 12, 1 << 4, 5, 7, 1, None, None, fake, None, 0, None)
+    assert rc == 1 and "int32 sources" in _err()
+    rc = lib.ravel_em_latest_k_resolve(None, None, nat.INT64, None,
+                                       1 << 20, 1 << 12, 1 << 4, 7, 1, fake, None, 0, None)
+    assert rc == 1 and "2^31" in _err()
+    rc = lib.ravel_em_latest_k_bwd(fake, fake, nat.FLOAT32, 1 << 20, 1 << 12, 1 << 4, 5, 1, 0,
+                                   fake, None, 0, None)
+    assert rc == 1 and "2^31" in _err()
+    rc = lib.ravel_em_sort_order(None, nat.INT64, None, 1 << 20, 1 << 12, 1 << 4, 7,
+                                 None, None, None, 0, None)
     assert rc == 1 and "2^31" in _err()
     # null pointers with a non-empty tape
     rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
@@ -155,3 +177,35 @@ def test_empty_tape_is_a_no_op():
     rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
                                    0, 3, 4, 5, 7, 1, None, None, None, None, 0, None)
     assert rc == 0
+
+
+def test_split_hook_and_split_workspaces():
+    lib = nat.library()
+    assert lib.ravel_em_set_split_slots(-1) == 1 and "split slots" in _err()
+    assert lib.ravel_em_set_split_slots(1 << 31) == 1
+    # a tape past 2^26 slots is sized for one range of rows: 2^31 records of
+    # 32768 rows x 65536 steps run in ranges of 1024 rows (2^26 records)
+    big = lib.ravel_em_latest_k_workspace(1 << 15, 1 << 16, 1, 4096, 1, 0, 0, 0)
+    rng = lib.ravel_em_latest_k_workspace(1 << 10, 1 << 16, 1, 4096, 1, 0, 0, 0)
+    assert big == rng > 0
+    assert lib.ravel_em_latest_k_workspace((1 << 10) + 1, 1 << 16, 1, 4096, 1, 0, 0, 0) == big
+    assert lib.ravel_em_seg_sum_workspace(1 << 15, 1 << 16, 1, 1, 4096, 0, 0, nat.FLOAT32) == \
+        lib.ravel_em_seg_sum_workspace(1 << 10, 1 << 16, 1, 1, 4096, 0, 0, nat.FLOAT32) > 0
+    # k = 4 over 2^29 records: ranges of 256 rows of 2^16 records; the sorted
+    # backward adds the range-local sources when it splits
+    assert lib.ravel_em_latest_k_bwd_workspace(8192, 1 << 15, 2, 1, 4, nat.FLOAT32, 0) > \
+        lib.ravel_em_latest_k_bwd_workspace(256, 1 << 15, 2, 1, 4, nat.FLOAT32, 0) > 0
+    # a single row past 2^26 slots runs whole
+    assert lib.ravel_em_latest_k_workspace(1, 1 << 28, 2, 4096, 1, 0, 0, 0) > big
+    # the hook: ranges of two rows size the workspace of a two-row tape
+    try:
+        assert lib.ravel_em_set_split_slots(2 * 64 * 3 * 4) == 0
+        assert lib.ravel_em_latest_k_workspace(7, 64, 3, 11, 4, 0, 0, 1) == \
+            lib.ravel_em_latest_k_workspace(2, 64, 3, 11, 4, 0, 0, 1)
+        assert lib.ravel_em_set_split_slots(2 * 64 * 3) == 0  # the sums count records
+        assert lib.ravel_em_seg_sum_workspace(7, 64, 3, 8, 11, 1, 0, nat.FLOAT32) == \
+            lib.ravel_em_seg_sum_workspace(2, 64, 3, 8, 11, 1, 0, nat.FLOAT32)
+    finally:
+        assert lib.ravel_em_set_split_slots(0) == 0
+    assert lib.ravel_em_latest_k_workspace(7, 64, 3, 11, 4, 0, 0, 1) > \
+        lib.ravel_em_latest_k_workspace(2, 64, 3, 11, 4, 0, 0, 1)
