@@ -18,14 +18,13 @@
  *
  * Tape sizes.  The reference's int64 key path has no size bound
  * (ravel_lm/ravel_memory.py:45-49, :159-174).  Here every (b, c) segment holds
- * records of one batch row, so the entry points that take a [B,T,C] tape
- * (except ravel_em_sort_order) run a tape whose slots B*T*C*k (records, for
- * the sums, the prefill and the addresses) pass 2^26 as consecutive ranges of
- * whole rows of at most 2^26 slots, on the same stream and workspace; their
- * *_workspace() queries size one range.  What must fit is one batch row:
- * T*C*k < 2^31.  Outputs that are int32 record indices (out_src, and the
- * sources that ravel_em_latest_k_bwd takes) need N < 2^31;
- * ravel_em_sort_order needs N < 2^31.
+ * records of one batch row, so the entry points that take a [B,T,C] tape run
+ * a tape whose slots B*T*C*k (records, for the sums, the sort order, the
+ * prefill and the addresses) pass 2^26 as consecutive ranges of whole rows of
+ * at most 2^26 slots, on the same stream and workspace; their *_workspace()
+ * queries size one range.  What must fit is one batch row: T*C*k < 2^31.
+ * Outputs that are int32 record indices (out_src, and the sources that
+ * ravel_em_latest_k_bwd takes) need N < 2^31.
  */
 #ifndef RAVEL_EM_H
 #define RAVEL_EM_H

@@ -840,11 +840,16 @@ int ravel_em_key_bits(int64_t B, int64_t T, int64_t C, int64_t A) {
 }
 
 size_t ravel_em_sort_order_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int has_mask) {
-  if (check_tape(B, T, C, A)) return 0;
-  const Tape tp = make_tape(B, T, C, A, has_mask != 0, kWrap);
+  if (check_rows(B, T, C, A, 1)) return 0;
+  const int64_t rows = split_rows(B, T * C);
+  const int64_t nb = B < rows ? B : rows;
+  const Tape tp = make_tape(nb, T, C, A, has_mask != 0, kWrap);
   Bump bp(nullptr);
   bp.off = sort_bytes(tp);
-  if (has_mask) bp.take<int64_t>((size_t)(B * T + 1));
+  if (has_mask) {
+    bp.take<int64_t>((size_t)(nb * T + 1));
+    bp.take<int64_t>(1);
+  }
   return bp.off;
 }
 
@@ -853,30 +858,43 @@ int ravel_em_sort_order(const void* write_addr, int addr_dtype, const uint8_t* w
                         int64_t* out_order, void* workspace, size_t workspace_bytes,
                         void* stream) {
   g_err.clear();
-  if (int rc = check_tape(B, T, C, A)) return rc;
+  if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_addr_dtype(addr_dtype)) return rc;
-  Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
-  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
+  const Tape full = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (full.n() == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!write_addr || !out_sorted_keys || !out_order) return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrIn wa;
   if (int rc = addr_in(write_addr, addr_dtype, C, &wa)) return rc;
   hipStream_t s = (hipStream_t)stream;
   const bool keys64 = ravel_em_key_bits(B, T, C, A) == 64;
-  auto run = [&](auto tag) -> int {
-    using U = decltype(tag);
-    Bump bp(workspace);
-    SortWs<U> sw = take_sort<U>(bp, tp);
-    tp.status = sw.status;
-    int64_t* vprefix = write_mask ? bp.take<int64_t>((size_t)(B * T + 1)) : nullptr;
-    if (int rc = check_ws(bp, workspace_bytes)) return rc;
-    U* sorted = nullptr;
-    hipError_t e = sort_call<U>(wa, write_mask, tp, sw, &sorted, s);
-    if (e != hipSuccess) return hip_fail(e, "sort");
-    e = emit_order<U>(sorted, write_mask, vprefix, tp, out_sorted_keys, keys64, out_order, s);
-    if (e != hipSuccess) return hip_fail(e, "emit order");
-    return RAVEL_EM_OK;
-  };
-  return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+  const int64_t rows = split_rows(B, T * C);
+  const int64_t nbmax = B < rows ? B : rows;
+  return split_batch(B, rows, workspace, workspace_bytes, s, [&](int64_t nb, int64_t b0) -> int {
+    Tape tp = full;
+    tp.B = nb;
+    const AddrIn w = addr_rows(wa, b0, T, C);
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    auto run = [&](auto tag) -> int {
+      using U = decltype(tag);
+      // The layout is that of the longest range, the same for every range:
+      // the carry word must stay where the earlier ranges left it.
+      Tape longest = full;
+      longest.B = nbmax;
+      Bump bp(workspace);
+      SortWs<U> sw = take_sort<U>(bp, longest);
+      tp.status = sw.status;
+      int64_t* vprefix = write_mask ? bp.take<int64_t>((size_t)(nbmax * T + 1)) : nullptr;
+      int64_t* carry = write_mask ? bp.take<int64_t>(1) : nullptr;
+      if (int rc = check_ws(bp, workspace_bytes)) return rc;
+      U* sorted = nullptr;
+      hipError_t e = sort_call<U>(w, wm, tp, sw, &sorted, s);
+      if (e != hipSuccess) return hip_fail(e, "sort");
+      e = emit_order<U>(sorted, wm, vprefix, tp, out_sorted_keys, keys64, out_order, s, b0, carry);
+      if (e != hipSuccess) return hip_fail(e, "emit order");
+      return RAVEL_EM_OK;
+    };
+    return tp.wide() ? run(uint64_t{}) : run(uint32_t{});
+  });
 }
 
 size_t ravel_em_latest_k_workspace(int64_t B, int64_t T, int64_t C, int64_t A, int64_t k,

@@ -232,10 +232,14 @@ hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp,
 size_t sort_counts_words(const Tape& tp);
 size_t sort_fused_words(const Tape& tp, size_t key_bytes);
 
-// Emit torch.sort-compatible (sorted_keys, order) for the valid records.
+// Emit torch.sort-compatible (sorted_keys, order) for the valid records of the
+// rows b0 .. b0 + tp.B - 1 of a tape (sorted: those rows' keys; the output
+// pointers are the whole tape's).  With a mask, carry_word (device) carries
+// the valid count of the earlier rows from one range to the next.
 template <typename U>
 hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, const Tape& tp,
-                      void* out_keys, bool keys64, int64_t* out_order, hipStream_t s);
+                      void* out_keys, bool keys64, int64_t* out_order, hipStream_t s,
+                      int64_t b0, int64_t* carry_word);
 
 // Latest-k source indices, int32, -1 for a missing slot.  link_same writes them
 // segment-major ([B,C,T,k], the record-major layout when C == 1);

@@ -191,11 +191,16 @@ __global__ __launch_bounds__(kSortThreads) void scatter_kernel(const U* __restri
 }
 
 // vprefix[x] = number of valid (b,t) before flat position x; x in [0, B*T].
+// out[i] = valid entries of m before i, plus *carry_word (0 when first); the
+// total is written to out[n] and back to *carry_word, so consecutive row
+// ranges of one tape count on from each other.
 __global__ __launch_bounds__(1024) void mask_prefix_kernel(const uint8_t* __restrict__ m,
-                                                          int64_t n, int64_t* __restrict__ out) {
+                                                          int64_t n, int64_t* __restrict__ out,
+                                                          int64_t* __restrict__ carry_word,
+                                                          int first) {
   __shared__ uint32_t tmp[1024 / kWave + 1];
   __shared__ int64_t carry;
-  if (threadIdx.x == 0) carry = 0;
+  if (threadIdx.x == 0) carry = first ? 0 : *carry_word;
   __syncthreads();
   for (int64_t base = 0; base < n; base += 1024) {
     const int64_t i = base + threadIdx.x;
@@ -207,14 +212,20 @@ __global__ __launch_bounds__(1024) void mask_prefix_kernel(const uint8_t* __rest
     if (threadIdx.x == 0) carry += total;
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[n] = carry;
+  if (threadIdx.x == 0) {
+    out[n] = carry;
+    *carry_word = carry;
+  }
 }
 
+// Rows of the tape from b0 on (the sorted keys of a row range); vprefix, when
+// given, counts the whole tape's valid steps.
 template <typename U, typename K>
 __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ sorted,
                                                         const int64_t* __restrict__ vprefix,
                                                         int64_t N, int64_t T, int64_t C, int64_t A,
-                                                        int tbits, K* __restrict__ out_keys,
+                                                        int tbits, int64_t b0,
+                                                        K* __restrict__ out_keys,
                                                         int64_t* __restrict__ out_order) {
   const U tmask = (U)((((uint64_t)1) << tbits) - 1);
   for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < N;
@@ -233,12 +244,12 @@ __global__ __launch_bounds__(256) void emit_order_kernel(const U* __restrict__ s
       nvb = vprefix[(b + 1) * T] - before;
       cidx = vprefix[b * T + t] * C + c;
     } else {
-      before = b * T;
+      before = (b0 + b) * T;
       nvb = T;
-      cidx = (b * T + t) * C + c;
+      cidx = ((b0 + b) * T + t) * C + c;
     }
     const int64_t P = before * C + c * nvb + i;
-    out_keys[P] = (K)(((b * C + c) * A + a) * (T + 1) + t);
+    out_keys[P] = (K)((((b0 + b) * C + c) * A + a) * (T + 1) + t);
     out_order[P] = cidx;
   }
 }
@@ -1529,9 +1540,10 @@ hipError_t sort_tape(const AddrIn& addr, const uint8_t* wmask, const Tape& tp, U
 
 template <typename U>
 hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, const Tape& tp,
-                      void* out_keys, bool keys64, int64_t* out_order, hipStream_t s) {
+                      void* out_keys, bool keys64, int64_t* out_order, hipStream_t s, int64_t b0,
+                      int64_t* carry_word) {
   if (wmask) {
-    mask_prefix_kernel<<<1, 1024, 0, s>>>(wmask, tp.B * tp.T, vprefix);
+    mask_prefix_kernel<<<1, 1024, 0, s>>>(wmask, tp.B * tp.T, vprefix, carry_word, b0 == 0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1540,10 +1552,10 @@ hipError_t emit_order(const U* sorted, const uint8_t* wmask, int64_t* vprefix, c
   const int64_t* vp = wmask ? vprefix : nullptr;
   if (keys64)
     emit_order_kernel<U, int64_t><<<grid, 256, 0, s>>>(sorted, vp, N, tp.T, tp.C, tp.A, tp.tbits,
-                                                       (int64_t*)out_keys, out_order);
+                                                       b0, (int64_t*)out_keys, out_order);
   else
     emit_order_kernel<U, int32_t><<<grid, 256, 0, s>>>(sorted, vp, N, tp.T, tp.C, tp.A, tp.tbits,
-                                                       (int32_t*)out_keys, out_order);
+                                                       b0, (int32_t*)out_keys, out_order);
   return hipGetLastError();
 }
 
@@ -1716,8 +1728,8 @@ template hipError_t sort_tape<uint64_t>(const AddrIn&, const uint8_t*, const Tap
                                         uint64_t*, uint32_t*, uint64_t**, hipStream_t, uint32_t*,
                                         int64_t, int32_t*);
 template hipError_t emit_order<uint32_t>(const uint32_t*, const uint8_t*, int64_t*, const Tape&,
-                                         void*, bool, int64_t*, hipStream_t);
+                                         void*, bool, int64_t*, hipStream_t, int64_t, int64_t*);
 template hipError_t emit_order<uint64_t>(const uint64_t*, const uint8_t*, int64_t*, const Tape&,
-                                         void*, bool, int64_t*, hipStream_t);
+                                         void*, bool, int64_t*, hipStream_t, int64_t, int64_t*);
 
 }  // namespace rem

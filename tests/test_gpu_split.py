@@ -25,7 +25,7 @@ import torch
 import oracle
 from ravel_em import (LayerAddresses, RavelLayerCache, causal_last_k_lookup,
                       causal_last_k_sources, causal_sum_lookup, fused_latest1_linear,
-                      literal_addresses_from_tokens)
+                      literal_addresses_from_tokens, sort_order)
 from ravel_em import _native as nat
 from test_gpu_sum import compare_sums, oracle_terms, sum_depth
 
@@ -157,6 +157,20 @@ def test_fused_linear_split(device):
     assert torch.allclose(g2, gb, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("B,T,C,A,masked", [(5, 37, 3, 11, False), (5, 37, 3, 11, True),
+                                             (3, 5000, 2, 300, True), (4, 3000, 3, 1 << 20, False)])
+def test_sort_order_split(device, B, T, C, A, masked):
+    w, _, _, m, host = tape(device, B, T, C, A, mask=masked, seed=11)
+    print(f"[split] sort order B={B} T={T} C={C} A={A} mask={masked}", flush=True)
+    base = sort_order(w, address_space=A, write_mask=m)
+    with split_slots(2 * T * C):
+        got = sort_order(w, address_space=A, write_mask=m)
+    assert torch.equal(got[0], base[0]) and torch.equal(got[1], base[1])
+    keys, order = oracle.sort_order(host[0], address_space=A, write_mask=host[3])
+    assert np.array_equal(got[0].cpu().numpy().astype(np.int64), keys)
+    assert np.array_equal(got[1].cpu().numpy(), order)
+
+
 @pytest.mark.parametrize("masked", [False, True])
 def test_prefill_split(device, masked):
     B, T, C, A, k, D = 6, 200, 3, 13, 4, 8
@@ -281,3 +295,13 @@ def test_latest1_and_sum_past_2p31_records(device):
         assert torch.equal(omask[b:b + 1].cpu(), tmask), f"row {b}"
         compare_sums(out[b:b + 1].cpu(), truth, scale, n, torch.float32,
                      sum_depth(T, 1, torch.float32), f"row {b} of 2^31 records")
+    del out, omask
+    keys, order = sort_order(w, address_space=A)
+    torch.cuda.synchronize()
+    assert keys.dtype == torch.int64 and keys.numel() == B * T * C
+    for b in check_rows:
+        wk, wo = oracle.sort_order(host_w[b], address_space=A)
+        sl = slice(b * T * C, (b + 1) * T * C)
+        # row b alone: its keys without the row's base, its order from 0
+        assert np.array_equal(keys[sl].cpu().numpy() - b * C * A * (T + 1), wk), f"row {b}"
+        assert np.array_equal(order[sl].cpu().numpy() - b * T * C, wo), f"row {b}"
