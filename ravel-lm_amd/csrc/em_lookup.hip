@@ -617,9 +617,9 @@ __global__ __launch_bounds__(kRowsThreads) void link_rows_lds_kernel(const U* __
   }
 }
 
-// Fill of n bytes: the 16-byte-aligned body with 16-byte stores (measured at
-// torch's fill rate, 6.8 TB/s on 4.3 GB; non-temporal stores were slower), the
-// unaligned head and tail byte by byte.
+// Fill of n bytes: the 16-byte-aligned body with streaming 16-byte stores
+// (torch's fill rate, about 6.8 TB/s on 4.3 GB), the unaligned head and tail
+// byte by byte.
 __global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ p, int64_t n,
                                                    int64_t head, int64_t body, uint8_t v) {
   const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
