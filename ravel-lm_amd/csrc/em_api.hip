@@ -381,6 +381,7 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
     return RAVEL_EM_OK;
   }
   U* sorted = nullptr;
+  bool mask_done = false;  // the transpose wrote the mask
   stage_begin(kStageSort, s);
   hipError_t e = sort_call<U>(wa, wmask, tp, sw, &sorted, s, nullptr, 0,
                               link && k == 1 ? src_seg : nullptr);
@@ -391,7 +392,8 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
     e = link_rows<U>(sorted, tp, (int)k, src, s);
   } else if (link) {
     if (sorted) e = link_same<U>(sorted, tp, (int)k, src_seg, s);  // else the sort linked
-    if (e == hipSuccess && src_seg != src) e = src_record_major(src_seg, tp, (int)k, src, s);
+    if (e == hipSuccess && src_seg != src)
+      e = src_record_major(src_seg, tp, (int)k, src, s, out_mask, &mask_done);
   } else {
     e = read_call<U>(sorted, wa, ra, tp, sw, (int)k, src, nullptr, s);
   }
@@ -399,8 +401,8 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   if (e != hipSuccess) return hip_fail(e, "resolve");
   stage_begin(kStageGather, s);
   // reads = writes and k == 1: every record is the source of at most one slot
-  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s,
-                  link && k == 1);
+  e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values,
+                  mask_done ? nullptr : out_mask, s, link && k == 1);
   stage_end(kStageGather, s);
   if (e != hipSuccess) return hip_fail(e, "gather");
   return RAVEL_EM_OK;

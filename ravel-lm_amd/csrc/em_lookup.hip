@@ -463,7 +463,8 @@ __global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __
 template <int LOGC>
 __global__ __launch_bounds__(256) void src_transpose_pow2_kernel(const int32_t* __restrict__ src_seg,
                                                                 int64_t T, int64_t ntt,
-                                                                int32_t* __restrict__ out) {
+                                                                int32_t* __restrict__ out,
+                                                                uint8_t* __restrict__ mask) {
   constexpr int C = 1 << LOGC;
   constexpr int TT = kTileWords >> LOGC;
   constexpr int ROW = TT + 4;  // padded head row, 16-byte aligned
@@ -499,6 +500,10 @@ __global__ __launch_bounds__(256) void src_transpose_pow2_kernel(const int32_t* 
       w.z = (uint32_t)lds[((f + 2) & (C - 1)) * ROW + ((f + 2) >> LOGC)];
       w.w = (uint32_t)lds[((f + 3) & (C - 1)) * ROW + ((f + 3) >> LOGC)];
       o[idx] = w;
+      if (mask)  // the slots' mask bytes in the same order, four per thread
+        ((uint32_t*)(mask + (b * T + t0) * C))[idx] =
+            ((int32_t)w.x >= 0 ? 1u : 0u) | ((int32_t)w.y >= 0 ? 1u << 8 : 0u) |
+            ((int32_t)w.z >= 0 ? 1u << 16 : 0u) | ((int32_t)w.w >= 0 ? 1u << 24 : 0u);
     }
   }
 }
@@ -738,7 +743,8 @@ hipError_t search_reads(const U* sorted, const AddrIn& raddr, const Tape& tp, in
 }
 
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
-                            hipStream_t s) {
+                            hipStream_t s, uint8_t* mask, bool* mask_done) {
+  if (mask_done) *mask_done = false;
   if (tp.n() == 0) return hipSuccess;
   if (k > kTileWords) return hipErrorInvalidValue;
   const bool vec = k == 1 && tp.C >= 2 && tp.C <= 16 && (tp.C & (tp.C - 1)) == 0 &&
@@ -748,12 +754,15 @@ hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32
     const int64_t ntt = (tp.T + (kTileWords >> logc) - 1) / (kTileWords >> logc);
     if (tp.B * ntt > INT32_MAX) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)(tp.B * ntt);
+    // the mask goes out with the sources when its 4-byte stores are aligned
+    uint8_t* m = mask && ((uintptr_t)mask & 3) == 0 ? mask : nullptr;
     switch (logc) {
-      case 1: src_transpose_pow2_kernel<1><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
-      case 2: src_transpose_pow2_kernel<2><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
-      case 3: src_transpose_pow2_kernel<3><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
-      default: src_transpose_pow2_kernel<4><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out); break;
+      case 1: src_transpose_pow2_kernel<1><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out, m); break;
+      case 2: src_transpose_pow2_kernel<2><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out, m); break;
+      case 3: src_transpose_pow2_kernel<3><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out, m); break;
+      default: src_transpose_pow2_kernel<4><<<blocks, 256, 0, s>>>(src_seg, tp.T, ntt, out, m); break;
     }
+    if (mask_done) *mask_done = m != nullptr;
     return hipGetLastError();
   }
   // Heads per tile: all of them up to 16 (a contiguous output run), time
