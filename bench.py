@@ -339,9 +339,10 @@ def main():
         fill_gbps = dst_buf.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
         del src_buf, dst_buf
 
-    # Gather kernel bytes: src read (4 B/slot), values + mask written, and one
-    # payload row read per valid slot.
-    gather_bytes = N * k * (4 + 1 + row_bytes) + valid_slots * row_bytes
+    # Gather kernel bytes: src read (4 B/slot), values written, and one payload
+    # row read per valid slot.  On this path (k = 1, reads = writes, C a power
+    # of two) the source transpose writes the mask bytes, not the gather.
+    gather_bytes = N * k * (4 + row_bytes) + valid_slots * row_bytes
     gather_gbps = gather_bytes / (gather_ms * 1e-3) / 1e9
     traffic = step_measured = None
     if os.path.exists(TRAFFIC_FILE) and not args.adversarial:  # measured for the uniform tape
