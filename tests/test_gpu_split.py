@@ -305,3 +305,27 @@ def test_latest1_and_sum_past_2p31_records(device):
         # row b alone: its keys without the row's base, its order from 0
         assert np.array_equal(keys[sl].cpu().numpy() - b * C * A * (T + 1), wk), f"row {b}"
         assert np.array_equal(order[sl].cpu().numpy() - b * T * C, wo), f"row {b}"
+
+
+@pytest.mark.parametrize("sep,masked", [(False, False), (True, True)])
+def test_static_entry_split(device, sep, masked):
+    """The entry point without a workspace runs split calls out of its static
+    scratch: same results as the workspace call, status word zero (folded over
+    the ranges)."""
+    lib = nat.library()
+    B, T, C, A, k, D = 5, 300, 2, 7, 2, 8
+    w, p, r, m, _ = tape(device, B, T, C, A, read=sep, mask=masked, D=D, seed=13)
+    print(f"[split] static entry sep={sep} mask={masked}", flush=True)
+    base = causal_last_k_sources(w, p, r, address_space=A, k=k, write_mask=m)
+    vals = torch.full((B, T, C, k, D), 7.0, device=device)
+    mask = torch.ones(B, T, C, k, dtype=torch.bool, device=device)
+    src = torch.full((B, T, C, k), -5, dtype=torch.int32, device=device)
+    status = torch.full((1,), 0xFFFF, dtype=torch.int32, device=device)
+    with split_slots(2 * T * C * k):
+        nat.check(lib.ravel_em_latest_k_fwd_static(
+            nat.ptr(w), nat.ptr(r), nat.addr_code(w.dtype), nat.ptr(m), nat.ptr(p),
+            nat.payload_code(p.dtype), B, T, C, D, A, k, nat.ptr(vals), nat.ptr(mask), nat.ptr(src),
+            nat.ptr(status), nat.stream_of(p)))
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    assert torch.equal(vals, base[0]) and torch.equal(mask, base[1]) and torch.equal(src, base[2])
