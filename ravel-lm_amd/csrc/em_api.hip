@@ -348,10 +348,6 @@ size_t sort_bytes(const Tape& tp) {
 
 // ---------------------------------------------------------- latest-k --
 
-struct LkPlan {
-  int32_t* src;
-};
-
 template <typename U>
 int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                  const void* payload, int64_t row_bytes, const Tape& tape, int64_t k,
@@ -363,7 +359,8 @@ int latest_k_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   SortWs<U> sw = take_sort<U>(bp, tp);
   tp.status = sw.status;
   // The link writes segment-major sources (src_seg), which one tiled
-  // transpose turns record-major; the read search writes them record-major.
+  // transpose turns record-major, writing the mask with them; the read search
+  // writes them record-major.
   int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
   int32_t* src_seg = link && tp.C > 1 ? bp.take<int32_t>((size_t)(tp.n() * k)) : src;
   if (int rc = check_ws(bp, wsb)) return rc;

@@ -285,8 +285,10 @@ bool gather_gemm_apply(int dtype, int64_t P, int64_t M, const void* payload, con
 hipError_t gather_gemm(const void* payload, const int32_t* src, const void* W, int dtype,
                        int64_t NR, int64_t C, int64_t P, int64_t M, void* out, hipStream_t s);
 // Segment-major sources -> record-major (a no-op layout change when C == 1).
-// With mask, the k == 1 tile transpose also writes the slots' mask bytes
-// (src >= 0) and sets *mask_done; other forms leave the mask to the caller.
+// k <= kTransposeMaxK (one time step's slots of a head fit the LDS tile).
+constexpr int kTransposeMaxK = 4096;
+// With mask, the transpose also writes the slots' mask bytes (src >= 0) and
+// sets *mask_done (the k == 1 tile form when the mask is 4-byte aligned).
 hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32_t* out,
                             hipStream_t s, uint8_t* mask = nullptr, bool* mask_done = nullptr);
 // Opt-in per-stage timing (host side): brackets each stage with HIP events on

@@ -237,7 +237,10 @@ constexpr int kSearchLdsBytes = 64 * 1024;
 constexpr int kSearchTile = 2048;
 constexpr int kSearchIlp = 4;
 
-template <typename U, typename AS>
+// KV > 0: k == KV slots per read, stored as one KV-word vector (the slots of a
+// read are contiguous; one 16-byte store touches one cache line where KV
+// word stores would each touch one per lane).  KV == 0: runtime k, word stores.
+template <typename U, typename AS, int KV>
 __global__ __launch_bounds__(256) void search_lds_kernel(
     const U* __restrict__ sorted, const AS raddr, int64_t T, int64_t C, int64_t A,
     int tbits, int trunc32, int k, int top, int64_t ntile, int64_t nseg,
@@ -297,21 +300,38 @@ __global__ __launch_bounds__(256) void search_lds_kernel(
       const int64_t r = (b * T + t0 + tl) * C + c;
       bool alive = true;
       int32_t first = -1;
-      for (int j = 0; j < k; ++j) {
-        int32_t v = -1;
+      // slot j of read r: the j-th latest earlier write of its address, or -1
+      auto slot = [&](int j) -> int32_t {
         const int q = lo[m] - 1 - j;
-        if (alive && q >= 0) {
-          const U uq = kk[q + (q >> 6)];
-          if ((int64_t)(uq >> tbits) == a[m] && (int64_t)(uq & tmask) < T) {
-            v = vbase + (int32_t)(uq & tmask) * Ci;
-            if (j == 0) first = (int32_t)(seg * T + q);
-          } else {
-            alive = false;
-          }
-        } else {
+        if (!alive || q < 0) {
           alive = false;
+          return -1;
         }
-        if (src) src[r * k + j] = v;
+        const U uq = kk[q + (q >> 6)];
+        if ((int64_t)(uq >> tbits) != a[m] || (int64_t)(uq & tmask) >= T) {
+          alive = false;
+          return -1;
+        }
+        if (j == 0) first = (int32_t)(seg * T + q);
+        return vbase + (int32_t)(uq & tmask) * Ci;
+      };
+      if constexpr (KV == 4) {
+        u32x4 w;
+        w.x = (uint32_t)slot(0);
+        w.y = (uint32_t)slot(1);
+        w.z = (uint32_t)slot(2);
+        w.w = (uint32_t)slot(3);
+        if (src) *(u32x4*)(src + r * 4) = w;
+      } else if constexpr (KV == 2) {
+        u32x2 w;
+        w.x = (uint32_t)slot(0);
+        w.y = (uint32_t)slot(1);
+        if (src) *(u32x2*)(src + r * 2) = w;
+      } else {
+        for (int j = 0; j < k; ++j) {
+          const int32_t v = slot(j);
+          if (src) src[r * k + j] = v;
+        }
       }
       if (spos) spos[r] = first;
     }
@@ -403,13 +423,14 @@ hipError_t gather_typed(const void* rows, const int32_t* src, int64_t nrows, int
 // tc heads x tt time steps per block through LDS: the reads are runs of tt*k
 // words of one segment, the writes runs of tc*k words of one time step (the
 // whole tile is one contiguous run when tc == C).  tc * tt * k <= kTileWords.
-constexpr int kTileWords = 4096;
+constexpr int kTileWords = kTransposeMaxK;
 
 // Launched with exactly 256 threads.
 __global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __restrict__ src_seg,
                                                               int64_t T, int64_t C, int k, int tc,
                                                               int tt, int64_t ntt, int64_t ntc,
-                                                              int32_t* __restrict__ out) {
+                                                              int32_t* __restrict__ out,
+                                                              uint8_t* __restrict__ mask) {
   __shared__ int32_t lds[kTileWords + 64];
   const int64_t tile = blockIdx.x;
   const int64_t ct = tile % ntc;
@@ -451,7 +472,10 @@ __global__ __launch_bounds__(256) void src_record_major_kernel(const int32_t* __
       const int rem = i - ti * ck;
       const int cc = rem / k;
       const int j = rem - cc * k;
-      out[((b * T + t0 + ti) * C + c0) * k + rem] = lds[cc * row + ti * k + j];
+      const int64_t o = ((b * T + t0 + ti) * C + c0) * k + rem;
+      const int32_t x = lds[cc * row + ti * k + j];
+      out[o] = x;
+      if (mask) mask[o] = x >= 0 ? 1 : 0;  // the slots' mask bytes in the same order
     }
   }
 }
@@ -727,10 +751,20 @@ hipError_t search_reads(const U* sorted, const AddrIn& raddr, const Tape& tp, in
     while ((int64_t)top * 2 <= tp.T) top *= 2;  // highest power of two <= T
     const int64_t ntile = (tp.T + kSearchTile - 1) / kSearchTile;
     const unsigned g = xcd_grid(tp.nseg() * ntile, 1, (int64_t)1 << 31);
+    // k of 4 or 2 with an aligned src: one vector store per read
+    const int kv = (k == 4 && ((uintptr_t)src & 15) == 0) ? 4
+                   : (k == 2 && ((uintptr_t)src & 7) == 0) ? 2 : 0;
     return with_addr(raddr, tp, [&](auto ra) {
-      search_lds_kernel<U, decltype(ra)><<<g, 256, lds, s>>>(
-          sorted, ra, tp.T, tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k, top, ntile, tp.nseg(),
-          src, spos);
+      auto launch = [&](auto kern) {
+        kern<<<g, 256, lds, s>>>(sorted, ra, tp.T, tp.C, tp.A, tp.tbits, tp.trunc32 ? 1 : 0, k,
+                                 top, ntile, tp.nseg(), src, spos);
+      };
+      if (kv == 4)
+        launch(search_lds_kernel<U, decltype(ra), 4>);
+      else if (kv == 2)
+        launch(search_lds_kernel<U, decltype(ra), 2>);
+      else
+        launch(search_lds_kernel<U, decltype(ra), 0>);
       return hipGetLastError();
     });
   }
@@ -774,7 +808,8 @@ hipError_t src_record_major(const int32_t* src_seg, const Tape& tp, int k, int32
   const int64_t blocks = tp.B * ntt * ntc;
   if (blocks > INT32_MAX) return hipErrorInvalidValue;
   src_record_major_kernel<<<(unsigned)blocks, 256, 0, s>>>(src_seg, tp.T, tp.C, k, tc, tt, ntt, ntc,
-                                                           out);
+                                                           out, mask);
+  if (mask_done) *mask_done = mask != nullptr;
   return hipGetLastError();
 }
 
