@@ -52,7 +52,7 @@ def parse():
                     help="with --suite: only these tape configs (cfg1, cfg1b, cfg2_float32, "
                          "cfg2_bfloat16, cfg3, cfg4, cfg4_adv)")
     ap.add_argument("--suite-ops", nargs="+", default=None, metavar="OP",
-                    help="with --suite: only these tape ops (latest_k, seg_sum)")
+                    help="with --suite: only these tape ops (latest_k, seg_sum, latest_k_sum)")
     ap.add_argument("--suite-iters", type=int, default=50, help="with --suite: timed calls per op")
     ap.add_argument("--suite-no-graphs", action="store_true",
                     help="with --suite: time the decode step eagerly only (no HIP graph capture)")
@@ -200,15 +200,15 @@ def suite_cpu_baseline(w, op, budget_s=6.0):
         med, n = timed(fn, 3)
         return {"value": B * T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
                 "sample": f"{n} full calls (address ops + lookup), median {med:.4f} s"}
-    if op in ("latest_k", "seg_sum"):
+    if op in ("latest_k", "seg_sum", "latest_k_sum"):
         write = w.write.cpu()
         read = None if w.read is None else w.read.cpu()
         payload = w.payload.cpu()
         B, T = write.shape[:2]
-        if op == "latest_k":
-            fn = lambda: torch_ref.latest_k(write, payload, read, address_space=w.address_space, k=w.k)
-        else:
-            fn = lambda: torch_ref.seg_sum(write, payload, read, address_space=w.address_space)
+        lk = lambda: torch_ref.latest_k(write, payload, read, address_space=w.address_space, k=w.k)
+        ss = lambda: torch_ref.seg_sum(write, payload, read, address_space=w.address_space)
+        # the reference layer's pair of calls with use_sum_read (model.py:366-386)
+        fn = {"latest_k": lk, "seg_sum": ss, "latest_k_sum": lambda: (lk(), ss())}[op]
         med, n = timed(fn, 3)
         return {"value": B * T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
                 "sample": f"{n} full calls, median {med:.4f} s"}

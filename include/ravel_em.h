@@ -308,6 +308,35 @@ int ravel_em_seg_sum_fwd(const void* write_addr, const void* read_addr, int addr
                          uint8_t* out_mask, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/*
+ * causal_last_k_lookup and causal_sum_lookup of one tape in one call: the pair
+ * that RavelMemoryLayer.forward makes when use_sum_read is set
+ * (ravel_lm/model.py:366-386: the latest-k lookup, then the segmented sum of
+ * the same write_addr, payload, read_addr and write_mask; the reference sorts
+ * the tape once in each, ravel_memory.py:151 and :216).  Arguments are those
+ * of ravel_em_latest_k_fwd plus the sum's outputs:
+ *   out_values [B,T,C,k,D], out_mask [B,T,C,k], out_src [B,T,C,k] or NULL
+ *   (as ravel_em_latest_k_fwd), out_sum [B,T,C,D], out_sum_mask [B,T,C]
+ *   (as ravel_em_seg_sum_fwd).
+ * Results equal the two separate calls' (values, masks and sources bit for
+ * bit; sums within the same accumulation bound).  The tape is sorted once
+ * where one kernel can emit both: tapes of T <= 4096 with k <= 8 (one launch
+ * sorts reads and writes in LDS, sums and writes the sources, a second gathers
+ * the values) and, for reads = writes without a write_mask and k = 1, longer
+ * tapes (one sort, then one walk writes the sums and the latest-1 values);
+ * other shapes run the two operators one after the other.  The workspace
+ * carries the status word as the sorting calls' do.
+ */
+size_t ravel_em_latest_k_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                       int64_t k, int has_read, int has_mask, int want_src,
+                                       int payload_dtype);
+int ravel_em_latest_k_sum_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                              const uint8_t* write_mask, const void* payload, int payload_dtype,
+                              int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, int64_t k,
+                              void* out_values, uint8_t* out_mask, int32_t* out_src,
+                              void* out_sum, uint8_t* out_sum_mask, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Backward of causal_sum_lookup (autograd of the cumsum path, ravel_memory.py:216-241). */
 size_t ravel_em_seg_sum_bwd_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
                                       int has_read, int has_mask, int payload_dtype);

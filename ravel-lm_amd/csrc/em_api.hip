@@ -573,6 +573,97 @@ size_t sum_ws_t(const Tape& tp, int64_t D, int dtype, bool direct, bool backward
   return bp.off;
 }
 
+// ----------------------------------------------- latest-k and sum --
+// The latest-k lookup and the segmented sum of one tape (the pair of calls of
+// ravel_lm/model.py:366-386) over one sort:
+//   short tapes: the merged sum kernel, whose LDS sort already orders reads
+//     and writes, also writes every read's latest-k sources; one gather makes
+//     the values;
+//   long tapes, reads = writes, k = 1: one full sort, then the walker's sum
+//     walk also stores each record's predecessor row (the latest-1 value);
+//   otherwise: the two operators one after the other on the same workspace,
+//     their status words ORed.
+__global__ void status_keep_kernel(uint32_t* __restrict__ hdr, int restore) {
+  if (threadIdx.x == 0) {
+    if (restore)
+      hdr[0] |= hdr[kStatusJointWord];
+    else
+      hdr[kStatusJointWord] = hdr[0];
+  }
+}
+
+template <typename U>
+int latest_k_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
+                     const void* payload, int dtype, const Tape& tape, int64_t D, int64_t k,
+                     void* out_values, uint8_t* out_mask, int32_t* out_src, void* out_sum,
+                     uint8_t* out_sum_mask, void* ws, size_t wsb, hipStream_t s) {
+  const int64_t row_bytes = D * dtype_size(dtype);
+  Tape tp = tape;
+  if (seg_sum_merged_applies(tp, D, dtype, payload, out_sum) &&
+      seg_sum_merged_sources_apply(tp, D, dtype, k)) {
+    Bump bp(ws);
+    SortWs<U> sw = take_sort<U>(bp, tp);
+    tp.status = sw.status;
+    int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
+    if (int rc = check_ws(bp, wsb)) return rc;
+    stage_begin(kStageSum, s);
+    AddrIn wd, rd;
+    hipError_t e = compact_addresses(wa, tp, sw.kb, &wd, s);
+    if (e == hipSuccess && ra) e = compact_addresses(*ra, tp, sw.ka, &rd, s);
+    if (e == hipSuccess)
+      e = seg_sum_merged(wd, ra ? &rd : nullptr, wmask, payload, dtype, tp, D, out_sum,
+                         out_sum_mask, s, src, k);
+    stage_end(kStageSum, s);
+    if (e != hipSuccess) return hip_fail(e, "segmented sum and sources");
+    stage_begin(kStageGather, s);
+    // reads = writes and k == 1: every record is the source of at most one slot
+    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s,
+                    !ra && k == 1);
+    stage_end(kStageGather, s);
+    if (e != hipSuccess) return hip_fail(e, "gather");
+    return RAVEL_EM_OK;
+  }
+  if (!ra && !wmask && k == 1 && seg_sum_joint_applies(tp, D, dtype, payload, out_sum, out_values)) {
+    Bump bp(ws);
+    SumWs<U> w = take_sum<U>(bp, tp, D, dtype, true, false);
+    tp.status = w.sw.status;
+    if (int rc = check_ws(bp, wsb)) return rc;
+    U* sorted = nullptr;
+    stage_begin(kStageSort, s);
+    hipError_t e = sort_call<U>(wa, nullptr, tp, w.sw, &sorted, s, (uint32_t*)w.walk,
+                                2 * w.walk_words);
+    stage_end(kStageSort, s);
+    if (e != hipSuccess) return hip_fail(e, "sort");
+    stage_begin(kStageSum, s);
+    e = seg_sum_joint<U>(sorted, payload, dtype, tp, D, out_sum, out_sum_mask, out_values,
+                         out_mask, out_src, w.walk, s);
+    stage_end(kStageSum, s);
+    if (e != hipSuccess) return hip_fail(e, "segmented sum and latest-1");
+    return RAVEL_EM_OK;
+  }
+  if (int rc = latest_k_run<U>(wa, ra, wmask, payload, row_bytes, tape, k, out_values, out_mask,
+                               out_src, ws, wsb, s))
+    return rc;
+  status_keep_kernel<<<1, 64, 0, s>>>((uint32_t*)ws, 0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "status word");
+  if (int rc = seg_sum_run<U>(wa, ra, wmask, payload, dtype, tape, D, out_sum, out_sum_mask, ws,
+                              wsb, s))
+    return rc;
+  status_keep_kernel<<<1, 64, 0, s>>>((uint32_t*)ws, 1);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "status word");
+  return RAVEL_EM_OK;
+}
+
+template <typename U>
+size_t latest_k_sum_ws_t(const Tape& tp, int64_t D, int dtype, int64_t k, bool link,
+                         bool want_src) {
+  const size_t a = latest_k_ws_t<U>(tp, k, link, want_src);
+  const size_t b = sum_ws_t<U>(tp, D, dtype, link, false);
+  return a > b ? a : b;
+}
+
 // ------------------------------------------- static scratch (no allocation) --
 // ravel_em_latest_k_fwd_static runs out of this array instead of a caller
 // workspace.  Each GPU holds its own copy from the library's load until the
@@ -744,7 +835,7 @@ extern "C" {
 
 const char* ravel_em_last_error(void) { return g_err.c_str(); }
 
-int ravel_em_abi_version(void) { return 3; }
+int ravel_em_abi_version(void) { return 4; }
 
 int ravel_em_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
                               void* stream) {
@@ -1164,6 +1255,69 @@ int ravel_em_latest_k_bwd(const int32_t* src, const void* grad_values, int paylo
   });
 }
 
+size_t ravel_em_latest_k_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
+                                       int64_t k, int has_read, int has_mask, int want_src,
+                                       int payload_dtype) {
+  if (k < 1 || D < 1 || check_rows(B, T, C, A, k) || check_payload_dtype(payload_dtype)) return 0;
+  const int64_t rows = split_rows(B, T * C * k);
+  const Tape tp = make_tape(B < rows ? B : rows, T, C, A, has_mask != 0, kWrap);
+  const bool link = !has_read && !has_mask;
+  return tp.wide() ? latest_k_sum_ws_t<uint64_t>(tp, D, payload_dtype, k, link, want_src != 0)
+                   : latest_k_sum_ws_t<uint32_t>(tp, D, payload_dtype, k, link, want_src != 0);
+}
+
+int ravel_em_latest_k_sum_fwd(const void* write_addr, const void* read_addr, int addr_dtype,
+                              const uint8_t* write_mask, const void* payload, int payload_dtype,
+                              int64_t B, int64_t T, int64_t C, int64_t D, int64_t A, int64_t k,
+                              void* out_values, uint8_t* out_mask, int32_t* out_src,
+                              void* out_sum, uint8_t* out_sum_mask, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (k < 1) return fail(RAVEL_EM_EINVAL, "k must be positive");
+  if (int rc = check_rows(B, T, C, A, k)) return rc;
+  if (int rc = check_addr_dtype(addr_dtype)) return rc;
+  if (int rc = check_payload_dtype(payload_dtype)) return rc;
+  if (D < 1) return fail(RAVEL_EM_EINVAL, "payload dim must be >= 1");
+  if (out_src && B * T * C > kMaxRecords)
+    return fail(RAVEL_EM_EINVAL, "int32 sources need B*T*C < 2^31 (out_src = NULL gives values "
+                                 "and mask of any tape)");
+  const Tape tp = make_tape(B, T, C, A, write_mask != nullptr, kWrap);
+  if (tp.n() == 0) return clear_status(workspace, workspace_bytes, stream);
+  if (!write_addr || !payload || !out_values || !out_mask || !out_sum || !out_sum_mask)
+    return fail(RAVEL_EM_EINVAL, "null pointer");
+  AddrPair ap;
+  if (int rc = addr_pair(write_addr, read_addr, addr_dtype, C, &ap)) return rc;
+  const int64_t row_bytes = D * dtype_size(payload_dtype);
+  hipStream_t s = (hipStream_t)stream;
+  return split_batch(B, split_rows(B, T * C * k), workspace, workspace_bytes, s,
+                     [&](int64_t nb, int64_t b0) -> int {
+    Tape t = tp;
+    t.B = nb;
+    const int64_t r0 = b0 * T * C;  // first record of the range
+    const AddrIn w = addr_rows(ap.w, b0, T, C);
+    AddrIn r;
+    if (ap.rp) r = addr_rows(*ap.rp, b0, T, C);
+    const AddrIn* rp = ap.rp ? &r : nullptr;
+    const uint8_t* wm = write_mask ? write_mask + b0 * T : nullptr;
+    const void* pl = at(payload, r0 * row_bytes);
+    void* ov = at(out_values, r0 * k * row_bytes);
+    uint8_t* om = out_mask + r0 * k;
+    int32_t* os = out_src ? out_src + r0 * k : nullptr;
+    void* osum = at(out_sum, r0 * row_bytes);
+    uint8_t* osm = out_sum_mask + r0;
+    int rc = t.wide()
+                 ? latest_k_sum_run<uint64_t>(w, rp, wm, pl, payload_dtype, t, D, k, ov, om, os,
+                                              osum, osm, workspace, workspace_bytes, s)
+                 : latest_k_sum_run<uint32_t>(w, rp, wm, pl, payload_dtype, t, D, k, ov, om, os,
+                                              osum, osm, workspace, workspace_bytes, s);
+    if (rc == RAVEL_EM_OK && os && b0 > 0) {
+      const hipError_t e = shift_sources(os, t.n() * k, r0, B * T * C, os, s);
+      if (e != hipSuccess) return hip_fail(e, "sources");
+    }
+    return rc;
+  });
+}
+
 size_t ravel_em_seg_sum_workspace(int64_t B, int64_t T, int64_t C, int64_t D, int64_t A,
                                   int has_read, int has_mask, int payload_dtype) {
   if (check_rows(B, T, C, A, 1) || D < 1) return 0;
@@ -1333,7 +1487,7 @@ int ravel_em_cache_prefill(const void* write_addr, int addr_dtype, const uint8_t
   g_err.clear();
   if (int rc = check_rows(B, T, C, A, 1)) return rc;
   if (int rc = check_cache(addr_dtype, payload_dtype, B, C, A, k, D, true)) return rc;
-  if (B * C == 0) return RAVEL_EM_OK;
+  if (B * C == 0) return clear_status(workspace, workspace_bytes, stream);
   if (!values || !filled || (B * T * C > 0 && (!write_addr || !payload)))
     return fail(RAVEL_EM_EINVAL, "null pointer");
   AddrIn wa;

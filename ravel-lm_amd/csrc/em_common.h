@@ -87,6 +87,8 @@ constexpr int kStatusSplitWord = 1;
 // words 2-3 of the status area: the merged sum kernel's start gate (a
 // launch sequence number and a count; a scheduling hint, never an error)
 constexpr int kStatusGateWord = 2;
+// word 4: the latest-k half's bits while the sum half of a joint call runs
+constexpr int kStatusJointWord = 4;
 
 // Compute units and wall-clock rate (kHz) of a device, queried once.
 struct DeviceShape {
@@ -310,9 +312,24 @@ hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& 
 // (ra null = reads at the write addresses), rows of whole 16-byte units.
 bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
                             const void* out);
+// With osrc, the same launch also writes every read's latest-k sources
+// (record-major [B,T,C,k] int32, -1 for an empty slot) when
+// seg_sum_merged_sources_apply holds (k <= 8).
+bool seg_sum_merged_sources_apply(const Tape& tp, int64_t D, int dtype, int64_t k);
 hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                           const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
-                          uint8_t* omask, hipStream_t s);
+                          uint8_t* omask, hipStream_t s, int32_t* osrc = nullptr, int64_t k = 0);
+// Forward sums and latest-1 lookup of reads = writes over one sorted tape in
+// one walker launch (seg_sum_joint_applies: rows of 1..64 16-byte units, a
+// power of two; 16-byte aligned rows): out_sum/omask as seg_sum's direct form,
+// out_values [B,T,C,1,D] and vmask [B,T,C,1] as the latest-1 lookup, vsrc
+// (optional) its int32 sources.  Same workspace as seg_sum.
+bool seg_sum_joint_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
+                           const void* out_sum, const void* out_values);
+template <typename U>
+hipError_t seg_sum_joint(const U* sorted, const void* payload, int dtype, const Tape& tp,
+                         int64_t D, void* out_sum, uint8_t* omask, void* out_values,
+                         uint8_t* vmask, int32_t* vsrc, uint64_t* walk, hipStream_t s);
 size_t seg_sum_chunks(const Tape& tp);
 size_t acc_bytes(int dtype);
 size_t seg_sum_walk_words(const Tape& tp, int64_t D, int dtype);

@@ -385,13 +385,21 @@ __device__ __forceinline__ void add_unit(Acc* acc, u32x4 x) {
   for (int j = 0; j < CPU; ++j) acc[j] += LoadF::load(cv.e[j]);
 }
 
+// VAL (the fast form, reads = writes): the final walk also writes every
+// record's latest-1 value, the row of the position before it in its run (the
+// row the walk has just added; +0.0 at a run start), into vout at the sum's
+// offset, the same mask byte into vmask and, with vsrc, that row's record id
+// (-1 at a run start): the latest-1 lookup of the same sorted tape with no
+// sort, link or gather of its own.
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
-          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT, bool FAST>
+          bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT, bool FAST,
+          bool VAL = false>
 __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
     const U* __restrict__ sorted, const XIn* __restrict__ in, int64_t T, int64_t C, int64_t D,
     int tbits, int G, int64_t nparts, XOut* __restrict__ out, uint8_t* __restrict__ omask,
     uint64_t* __restrict__ status, uint64_t* __restrict__ tickets, uint32_t* __restrict__ err,
-    int64_t nout) {
+    int64_t nout, XOut* __restrict__ vout = nullptr, uint8_t* __restrict__ vmask = nullptr,
+    int32_t* __restrict__ vsrc = nullptr) {
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
   using OutV = typename Unit<CPU * (int)sizeof(XOut)>::T;
   constexpr int NWMAX = kWalkThreads;  // walkers when G == 1
@@ -404,7 +412,9 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   // FAST (forward exclusive sums by record, rows at 32-bit offsets of the
   // segment's base): one code word per position, walks without branches
   static_assert(!FAST || (!REV && !IN_SORTED && !INCL && !OUT_SORTED && !RT), "fast form");
+  static_assert(!VAL || (FAST && WMASK), "values ride on the fast form");
   __shared__ __align__(16) uint32_t cw[FAST ? kPartPos : 4];
+  __shared__ uint32_t s_ptime;  // VAL: time of the position before the part
   // Exclusive forward sums never add the last row of a run to any output:
   // those rows are not loaded (on a uniform tape most runs are one record).
   constexpr bool SKIP_LAST = !INCL && !REV;
@@ -433,9 +443,11 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
       start = (kk[i] >> tbits) != (kk[i - 1] >> tbits);
     } else if (wi == 0) {
       start = true;
+      if (VAL) s_ptime = 0u;
     } else {
       const U prev = sk[REV ? (T - wi) : (wi - 1)];
       start = (kk[0] >> tbits) != (prev >> tbits);
+      if (VAL) s_ptime = (uint32_t)(prev & tmask);
     }
     st[i] = start ? 1 : 0;
   }
@@ -482,6 +494,11 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
   const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((unsigned char*)out + (int64_t)vbase * G * 16), 0, ext, kRsrcWord3);
   Acc acc[CPU];
+  // VAL: the row of the item before the next one (zeros where not loaded)
+  u32x4 vprev = {0u, 0u, 0u, 0u};
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(VAL ? (unsigned char*)vout + (int64_t)vbase * G * 16 : (unsigned char*)vout), 0,
+      VAL ? ext : 0, kRsrcWord3);
   // Items [from, to) in whole batches from the one holding `from` (items
   // outside are pads): a run start resets the sum, every position stores the
   // sum before its own row (STORE), every needed row is added.
@@ -515,6 +532,13 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
           __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XOut, StoreF, Acc, CPU>(acc), ors,
                                                  (__umul24(k, tstride) + v16) | (k & kCodeNoStore), 0,
                                                  aux);
+        if (STORE && VAL) {
+          const u32x4 z = {0u, 0u, 0u, 0u};
+          __builtin_amdgcn_raw_buffer_store_b128(stt ? z : vprev, vrs,
+                                                 (__umul24(k, tstride) + v16) | (k & kCodeNoStore), 0,
+                                                 aux);
+          vprev = x[m];
+        }
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
       }
     }
@@ -612,15 +636,38 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
   if constexpr (FAST) {
+    if constexpr (VAL) {
+      // the row before the range's first item, when that item continues a run
+      if (rs < re) {
+        const uint32_t pc = rs > 0 ? cw[rs - 1] : s_ptime;
+        const bool cont = (cw[rs] & kCodeStart) == 0;  // false at p0 == 0
+        vprev = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, (__umul24(pc, tstride) + v16) | (cont ? 0u : kCodeNoLoad), 0, kBufNontemporal);
+      }
+    }
     walk_fast(rs, re, std::true_type{});
     if (WMASK) {  // a record's mask: some earlier record of its run (byte stores after the walk)
       __syncthreads();
       const __amdgpu_buffer_rsrc_t mrs =
           __builtin_amdgcn_make_buffer_rsrc((void*)(omask + vbase), 0, (int)(T * C), kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t vmrs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(VAL ? vmask + vbase : vmask), 0, VAL ? (int)(T * C) : 0, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(VAL && vsrc ? vsrc + vbase : vsrc), 0, VAL && vsrc ? (int)(T * C * 4) : 0,
+          kRsrcWord3);
       for (int i = tid; i < n; i += kWalkThreads) {
         const uint32_t k = cw[i];
-        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)((k & kCodeStart) ? 0 : 1), mrs,
-                                             (k & kCodeTime) * (uint32_t)C, 0, 0);
+        const uint8_t has = (k & kCodeStart) ? 0 : 1;
+        const uint32_t moff = (k & kCodeTime) * (uint32_t)C;
+        __builtin_amdgcn_raw_buffer_store_b8(has, mrs, moff, 0, 0);
+        if (VAL) {
+          __builtin_amdgcn_raw_buffer_store_b8(has, vmrs, moff, 0, 0);
+          if (vsrc) {
+            const uint32_t pt = i > 0 ? (cw[i - 1] & kCodeTime) : s_ptime;
+            const int32_t sr = has ? vbase + (int32_t)pt * Ci : -1;
+            __builtin_amdgcn_raw_buffer_store_b32((uint32_t)sr, srs, moff * 4u, 0, 0);
+          }
+        }
       }
     }
     return;
@@ -675,6 +722,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 //      a fold over the walkers, then the walk): writes add their payload row,
 //      each read stores the running sum and the mask (some write before it).
 // So the prefix rows are never stored and re-read, and reads need no search.
+// With KS > 0 the walk also emits every read's latest-k sources (k <= KS): each
+// walker keeps the times of the last KS writes of its run in registers, newest
+// first, and a read stores k record ids (-1 past the run's writes), the
+// search of ravel_memory.py:159-168 without a search.
 constexpr int kMergedThreads = 512;  // two blocks per CU (LDS and registers)
 constexpr int kMergedItems = 8192;  // 2T
 constexpr int kMergedLr = 4096;     // addresses of the last-read table
@@ -688,6 +739,10 @@ constexpr int kMergedUnion = 40960;
 constexpr int kMergedMaskOff = 32768;
 // the walkers' first run starts (at most kMergedThreads ints), between the two
 constexpr int kMergedStartOff = 20480;
+// the walkers' tail rings of write times and their counts (long runs with
+// sources only), after the first run starts and below the mask bytes
+constexpr int kMergedRingOff = kMergedStartOff + kMergedThreads * 4;
+constexpr int kMergedRingBytes = kMergedMaskOff - kMergedRingOff;
 static_assert(kMergedMaskOff + kMergedItems / 2 + 1 <= kMergedUnion, "mask bytes fit");
 
 // Start gate of the merged kernel.  With every block resident at once, all
@@ -753,14 +808,43 @@ __device__ __forceinline__ int64_t addr_col_value(const AddrCol& col, uint32_t t
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int ITEMS, typename XIn, typename Acc, typename LoadF, typename StoreF>
+// Sources of one read: slot j < min(k, cnt) is record ring[j], the others -1;
+// k int32 words at byte `off` of the rsrc (an offset at or past 2^30 stores
+// nothing).  k == KS stores whole vectors.
+template <int KS>
+__device__ __forceinline__ void store_sources(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                              const uint32_t* ring, int cnt, int k) {
+  int32_t v[KS];
+#pragma unroll
+  for (int j = 0; j < KS; ++j) v[j] = j < cnt ? (int32_t)ring[j] : -1;
+  if (KS == 1 || k == KS) {
+    if constexpr (KS == 1) {
+      __builtin_amdgcn_raw_buffer_store_b32((uint32_t)v[0], rs, off, 0, 0);
+    } else if constexpr (KS == 2) {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)v[0], (uint32_t)v[1]}, rs, off, 0, 0);
+    } else {
+#pragma unroll
+      for (int q = 0; q < KS / 4; ++q)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{(uint32_t)v[4 * q], (uint32_t)v[4 * q + 1], (uint32_t)v[4 * q + 2],
+                  (uint32_t)v[4 * q + 3]},
+            rs, off + 16u * (uint32_t)q, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+      if (j < k) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)v[j], rs, off + 4u * (uint32_t)j, 0, 0);
+  }
+}
+
+template <int ITEMS, int KS, typename XIn, typename Acc, typename LoadF, typename StoreF>
 __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void segsum_merged_kernel(
     const void* __restrict__ waddr, int wkind, const void* __restrict__ raddr, int rkind,
     const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int trunc32, int tbits,
     int npass, int G, int64_t nseg, const XIn* __restrict__ payload,
     XIn* __restrict__ out, uint8_t* __restrict__ omask, uint32_t* __restrict__ status,
     uint32_t* __restrict__ gate, uint32_t tag, uint32_t gate_lo, uint32_t gate_hi,
-    uint32_t gate_target, uint32_t gate_ticks) {
+    uint32_t gate_target, uint32_t gate_ticks, int32_t* __restrict__ osrc, int kslots) {
   constexpr int NT = kMergedThreads;
   constexpr int NWV = NT / kWave;
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
@@ -929,6 +1013,22 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   uint8_t* hm = (uint8_t*)(un + kMergedMaskOff);
   Acc acc[CPU];
   bool hasw = false;
+  // KS > 0: the record ids of the run's last KS writes (ring[0] the newest)
+  // and how many of them belong to the run; the sources of a read (k int32
+  // words, record-major) leave from lane v == 0 of its walker.  Pads count as
+  // writes here; they only ever stand before a run start or after the walk's
+  // items.
+  constexpr int KR = KS > 0 ? KS : 1;
+  uint32_t ring[KR];
+  int rcnt = 0;
+#pragma unroll
+  for (int j = 0; j < KR; ++j) ring[j] = 0u;
+  const int32_t rbase32 = (int32_t)rbase, Ci = (int32_t)C;
+  const uint32_t sstride = (uint32_t)(C * kslots * 4);
+  const uint32_t slane = v == 0 ? 0u : 0x80000000u;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(osrc ? osrc + rbase * kslots : osrc), 0, KS > 0 ? (int)(T * sstride) : 0,
+      kRsrcWord3);
   // Items [from, to), in whole batches from the one holding `from` (items
   // outside are pads): a run start resets the sum and the has-a-write flag, a
   // loaded write adds its row, a read (STORE) stores the sum and the flag.
@@ -966,6 +1066,17 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
                                                  (__umul24(k, tstride) + v16) | ns, 0, 0);
           hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = hasw ? 1 : 0;
         }
+        if constexpr (KS > 0) {
+          rcnt = st ? 0 : rcnt;
+          const bool wr = k & kCodeNoStore;
+          if (STORE)
+            store_sources<KS>(srs, (__umul24(k, sstride) | (k & kCodeNoStore)) | slane, ring, rcnt,
+                              kslots);
+#pragma unroll
+          for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
+          ring[0] = wr ? (uint32_t)(rbase32 + (int32_t)__umul24(k, (uint32_t)Ci)) : ring[0];
+          rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
+        }
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
         hasw = hasw || !(k & kCodeNoLoad);
       }
@@ -1001,6 +1112,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
     hasw = false;
+    rcnt = 0;
     if (a0 < re) walk(a0, a1, std::true_type{});
   } else {
   // tail: from the range's last run start (or its start) to its end
@@ -1013,11 +1125,22 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   }
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
+  rcnt = 0;
   walk(last >= 0 ? last : rs, re, std::false_type{});
   const bool hwt = hasw;
   const int ncol = G * CPU;  // == D
   Acc* tl = (Acc*)un;        // [walker][column]; the counters and table are dead
+  // KS > 0: each walker's tail ring ([walker][KS] times, then [walker] counts)
+  uint32_t* rt = (uint32_t*)(un + kMergedRingOff);
+  int* rc = (int*)(rt + NW * KR);
   __syncthreads();
+  if constexpr (KS > 0) {
+    if (v == 0) {
+#pragma unroll
+      for (int j = 0; j < KR; ++j) rt[w * KR + j] = ring[j];
+      rc[w] = rcnt;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < CPU; ++j) tl[w * ncol + v * CPU + j] = acc[j];
   if (v == 0) {
@@ -1075,6 +1198,22 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
   hasw = hwin[w] != 0;
+  if constexpr (KS > 0) {
+    // the ring carried into the range: the newest writes of the earlier
+    // walkers' tails, back to one that holds a run start (its tail starts
+    // there) or until KS are found
+    rcnt = 0;
+    for (int w2 = w - 1; w2 >= 0 && rcnt < KS; --w2) {
+      const int n2w = rc[w2];
+#pragma unroll
+      for (int j = 0; j < KR; ++j) {
+        const int src_j = j - rcnt;  // entry of w2's ring that lands in slot j
+        if (src_j >= 0 && src_j < n2w) ring[j] = rt[w2 * KR + src_j];
+      }
+      rcnt = rcnt + n2w < KS ? rcnt + n2w : KS;
+      if (hs[w2]) break;
+    }
+  }
   walk(rs, re, std::true_type{});
   }
   __syncthreads();
@@ -1094,10 +1233,20 @@ bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, cons
          tp.C * row_bytes < ((int64_t)1 << 24) && tp.T * tp.C * row_bytes <= ((int64_t)1 << 30);
 }
 
+// Ring size of the merged kernel's latest-k sources (0: none).
+int merged_ring(int64_t k) { return k < 1 ? 0 : (k == 1 ? 1 : (k <= 4 ? 4 : 8)); }
+
+bool merged_sources_apply(const Tape& tp, int64_t row_bytes, int64_t k) {
+  const int64_t NW = kMergedThreads / (row_bytes / 16);
+  const int KS = merged_ring(k);
+  return k >= 1 && k <= 8 && NW * (KS + 1) * 4 <= kMergedRingBytes &&
+         tp.T * tp.C * k * 4 <= ((int64_t)1 << 30);
+}
+
 template <int DT>
 hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                             const void* payload, const Tape& tp, int64_t D, void* out,
-                            uint8_t* omask, hipStream_t s) {
+                            uint8_t* omask, int32_t* osrc, int k, hipStream_t s) {
   using E = Elem<DT>;
   using S = typename E::store_t;
   using Acc = typename E::acc_t;
@@ -1116,15 +1265,25 @@ hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* w
   static std::atomic<uint32_t> launches{0};
   const uint32_t tag = (launches.fetch_add(1, std::memory_order_relaxed) + 1u) & 0xffffu;
   uint32_t* gate = tp.status + kStatusGateWord;
-#define REM_MG(IT)                                                                           \
-  segsum_merged_kernel<IT, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                     \
+#define REM_MG(IT, KS)                                                                       \
+  segsum_merged_kernel<IT, KS, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                 \
       wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
       tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
-      tag, gate_lo, gate_hi, target, ticks)
-  if (2 * tp.T <= 4 * kMergedThreads)
-    REM_MG(4);
-  else
-    REM_MG(16);
+      tag, gate_lo, gate_hi, target, ticks, osrc, k)
+#define REM_MG_KS(IT)                           \
+  switch (osrc ? merged_ring(k) : 0) {          \
+    case 0: REM_MG(IT, 0); break;               \
+    case 1: REM_MG(IT, 1); break;               \
+    case 4: REM_MG(IT, 4); break;               \
+    default: REM_MG(IT, 8); break;              \
+  }
+  if (osrc && !merged_sources_apply(tp, G * 16, k)) return hipErrorInvalidValue;
+  if (2 * tp.T <= 4 * kMergedThreads) {
+    REM_MG_KS(4);
+  } else {
+    REM_MG_KS(16);
+  }
+#undef REM_MG_KS
 #undef REM_MG
   return hipGetLastError();
 }
@@ -1237,6 +1396,40 @@ hipError_t seg_sum_bwd_t(const U* sorted, const int32_t* spos, const void* grad_
       sorted, (const G*)gacc, tp, D, (S*)grad_payload, nullptr, (Acc*)tail, flag, (Acc*)carry, walk, s);
 }
 
+// Forward sums and latest-1 values of reads = writes in one walk (the fast
+// walker form with VAL).
+bool joint_walk_applies(const Tape& tp, int64_t row_bytes, const void* payload, const void* out,
+                        const void* vout) {
+  const int64_t G = row_bytes / 16;
+  return row_bytes % 16 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
+         (((uintptr_t)payload | (uintptr_t)out | (uintptr_t)vout) & 15) == 0 &&
+         tp.T <= ((int64_t)1 << 24) && tp.C * row_bytes < ((int64_t)1 << 24) &&
+         tp.T * tp.C * row_bytes <= ((int64_t)1 << 30) &&
+         tp.nseg() * ((tp.T + kPartPos - 1) / kPartPos) <= INT32_MAX;
+}
+
+template <int DT, typename U>
+hipError_t seg_sum_joint_t(const U* sorted, const void* payload, const Tape& tp, int64_t D,
+                           void* out_sum, uint8_t* omask, void* out_values, uint8_t* vmask,
+                           int32_t* vsrc, uint64_t* walk, hipStream_t s) {
+  using E = Elem<DT>;
+  using S = typename E::store_t;
+  using Acc = typename E::acc_t;
+  const int64_t row_bytes = D * (int64_t)sizeof(S);
+  if (!tp.status || !walk || !joint_walk_applies(tp, row_bytes, payload, out_sum, out_values))
+    return hipErrorInvalidValue;
+  const int64_t G = row_bytes / 16;
+  const int64_t nparts = (tp.T + kPartPos - 1) / kPartPos;
+  const int64_t blocks = tp.nseg() * nparts;
+  uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
+  segsum_walk_kernel<U, S, S, Acc, E, E, false, false, false, false, true, false, true, true>
+      <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, (const S*)payload, tp.T, tp.C, D,
+                                                 tp.tbits, (int)G, nparts, (S*)out_sum, omask,
+                                                 walk, tickets, tp.status, 0, (S*)out_values,
+                                                 vmask, vsrc);
+  return hipGetLastError();
+}
+
 template <int DT, typename U>
 hipError_t run_totals_t(const U* sorted, const void* rows, const Tape& tp, int64_t D, int64_t nout,
                         void* out, void* tail, uint8_t* flag, void* carry, uint64_t* walk,
@@ -1300,15 +1493,45 @@ bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* pa
   return merged_applies(tp, D * dtype_size(dtype), payload, out);
 }
 
+bool seg_sum_joint_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
+                           const void* out_sum, const void* out_values) {
+  return joint_walk_applies(tp, D * dtype_size(dtype), payload, out_sum, out_values);
+}
+
+template <typename U>
+hipError_t seg_sum_joint(const U* sorted, const void* payload, int dtype, const Tape& tp,
+                         int64_t D, void* out_sum, uint8_t* omask, void* out_values,
+                         uint8_t* vmask, int32_t* vsrc, uint64_t* walk, hipStream_t s) {
+  switch (dtype) {
+    case kF32: return seg_sum_joint_t<kF32, U>(sorted, payload, tp, D, out_sum, omask, out_values, vmask, vsrc, walk, s);
+    case kF64: return seg_sum_joint_t<kF64, U>(sorted, payload, tp, D, out_sum, omask, out_values, vmask, vsrc, walk, s);
+    case kBF16: return seg_sum_joint_t<kBF16, U>(sorted, payload, tp, D, out_sum, omask, out_values, vmask, vsrc, walk, s);
+    case kF16: return seg_sum_joint_t<kF16, U>(sorted, payload, tp, D, out_sum, omask, out_values, vmask, vsrc, walk, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template hipError_t seg_sum_joint<uint32_t>(const uint32_t*, const void*, int, const Tape&,
+                                            int64_t, void*, uint8_t*, void*, uint8_t*, int32_t*,
+                                            uint64_t*, hipStream_t);
+template hipError_t seg_sum_joint<uint64_t>(const uint64_t*, const void*, int, const Tape&,
+                                            int64_t, void*, uint8_t*, void*, uint8_t*, int32_t*,
+                                            uint64_t*, hipStream_t);
+
+bool seg_sum_merged_sources_apply(const Tape& tp, int64_t D, int dtype, int64_t k) {
+  return merged_sources_apply(tp, D * dtype_size(dtype), k);
+}
+
 hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                           const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
-                          uint8_t* omask, hipStream_t s) {
+                          uint8_t* omask, hipStream_t s, int32_t* osrc, int64_t k) {
   if (!tp.status) return hipErrorInvalidValue;
+  const int kk = (int)k;
   switch (dtype) {
-    case kF32: return seg_sum_merged_t<kF32>(wa, ra, wmask, payload, tp, D, out, omask, s);
-    case kF64: return seg_sum_merged_t<kF64>(wa, ra, wmask, payload, tp, D, out, omask, s);
-    case kBF16: return seg_sum_merged_t<kBF16>(wa, ra, wmask, payload, tp, D, out, omask, s);
-    case kF16: return seg_sum_merged_t<kF16>(wa, ra, wmask, payload, tp, D, out, omask, s);
+    case kF32: return seg_sum_merged_t<kF32>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
+    case kF64: return seg_sum_merged_t<kF64>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
+    case kBF16: return seg_sum_merged_t<kBF16>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
+    case kF16: return seg_sum_merged_t<kF16>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -14,6 +14,7 @@ from .fused import fused_latest1_linear
 from .ravel_memory import (
     RavelLayerCache,
     _composite_key_dtype,
+    causal_last_k_and_sum_lookup,
     causal_last_k_lookup,
     causal_last_k_sources,
     causal_sum_lookup,
@@ -24,6 +25,7 @@ __all__ = [
     "LayerAddresses",
     "RavelLayerCache",
     "_composite_key_dtype",
+    "causal_last_k_and_sum_lookup",
     "causal_last_k_lookup",
     "causal_last_k_sources",
     "causal_sum_lookup",

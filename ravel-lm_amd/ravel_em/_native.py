@@ -80,6 +80,14 @@ SIGNATURES = {
     "ravel_em_latest_k_bwd": (
         _i, [_vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i, _vp, _vp, _sz, _vp]
     ),
+    "ravel_em_latest_k_sum_workspace": (
+        _sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i]
+    ),
+    "ravel_em_latest_k_sum_fwd": (
+        _i,
+        [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+         _vp, _sz, _vp],
+    ),
     "ravel_em_seg_sum_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
     "ravel_em_seg_sum_fwd": (
         _i, [_vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]

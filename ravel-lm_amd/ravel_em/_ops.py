@@ -237,6 +237,97 @@ def _seg_sum_grad(ctx, grad_sum, _grad_mask):
 seg_sum.register_autograd(_seg_sum_grad, setup_context=_seg_sum_setup)
 
 
+# ------------------------------------------------------ latest-k + sum --
+
+
+def latest_k_sum_impl(
+    write_addresses: Tensor,
+    payloads: Tensor,
+    read_addresses: Optional[Tensor],
+    write_mask: Optional[Tensor],
+    address_space: int,
+    k: int,
+    want_src: bool,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The body of ravel_em::latest_k_sum (also called directly, see eager):
+    (values, mask, src, sum, sum_mask) of one tape in one C call."""
+    lib = nat.library()
+    B, T, C = write_addresses.shape
+    D = payloads.shape[-1]
+    dev = payloads.device
+    values = payloads.new_empty(B, T, C, k, D)
+    mask = torch.empty(B, T, C, k, dtype=torch.bool, device=dev)
+    src = torch.empty((B, T, C, k) if want_src else (0,), dtype=torch.int32, device=dev)
+    out = payloads.new_empty(B, T, C, D)
+    smask = torch.empty(B, T, C, dtype=torch.bool, device=dev)
+    code = nat.payload_code(payloads.dtype)
+    nbytes = lib.ravel_em_latest_k_sum_workspace(
+        B, T, C, D, address_space, k, int(read_addresses is not None), int(write_mask is not None),
+        int(want_src), code)
+    ws = nat.workspace(nbytes, dev)
+    _call(
+        lib.ravel_em_latest_k_sum_fwd,
+        nat.ptr(write_addresses), nat.ptr(read_addresses), nat.addr_code(write_addresses.dtype),
+        nat.ptr(write_mask), nat.ptr(payloads), code, B, T, C, D, address_space, k,
+        nat.ptr(values), nat.ptr(mask), nat.ptr(src) if want_src else None, nat.ptr(out),
+        nat.ptr(smask), nat.ptr(ws), ws.numel(), nat.stream_of(payloads),
+    )
+    nat.after_call(ws)
+    return values, mask, src, out, smask
+
+
+@torch.library.custom_op("ravel_em::latest_k_sum", mutates_args=())
+def latest_k_sum(
+    write_addresses: Tensor,
+    payloads: Tensor,
+    read_addresses: Optional[Tensor],
+    write_mask: Optional[Tensor],
+    address_space: int,
+    k: int,
+    want_src: bool,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return latest_k_sum_impl(write_addresses, payloads, read_addresses, write_mask, address_space,
+                             k, want_src)
+
+
+@latest_k_sum.register_fake
+def _latest_k_sum_fake(write_addresses, payloads, read_addresses, write_mask, address_space, k,
+                       want_src):
+    B, T, C = write_addresses.shape
+    D = payloads.shape[-1]
+    dev = payloads.device
+    return (
+        payloads.new_empty(B, T, C, k, D),
+        torch.empty(B, T, C, k, dtype=torch.bool, device=dev),
+        torch.empty((B, T, C, k) if want_src else (0,), dtype=torch.int32, device=dev),
+        payloads.new_empty(B, T, C, D),
+        torch.empty(B, T, C, dtype=torch.bool, device=dev),
+    )
+
+
+def _latest_k_sum_setup(ctx, inputs, output):
+    write_addresses, payloads, read_addresses, write_mask, address_space, k, want_src = inputs
+    _, mask, src, _, smask = output
+    ctx.save_for_backward(src, write_addresses, read_addresses, write_mask)
+    ctx.chain = read_addresses is None and write_mask is None
+    ctx.want_src = want_src
+    ctx.address_space = address_space
+    ctx.mark_non_differentiable(mask, src, smask)
+
+
+def _latest_k_sum_grad(ctx, grad_values, _grad_mask, _grad_src, grad_sum, _grad_smask):
+    src, write_addresses, read_addresses, write_mask = ctx.saved_tensors
+    if not ctx.want_src:
+        raise RuntimeError("ravel_em.latest_k_sum was called without sources; cannot differentiate")
+    grad_payload = latest_k_backward(src, grad_values, ctx.chain)
+    grad_payload = grad_payload + seg_sum_backward(write_addresses, read_addresses, write_mask,
+                                                   grad_sum, ctx.address_space)
+    return None, grad_payload, None, None, None, None, None
+
+
+latest_k_sum.register_autograd(_latest_k_sum_grad, setup_context=_latest_k_sum_setup)
+
+
 # ------------------------------------------------------- direct C calls --
 
 

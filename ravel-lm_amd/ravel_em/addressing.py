@@ -400,6 +400,72 @@ def _seg_sum_gen_grad(ctx, grad_sum, _grad_mask):
 seg_sum_gen.register_autograd(_seg_sum_gen_grad, setup_context=_seg_sum_gen_setup)
 
 
+@torch.library.custom_op("ravel_em::latest_k_sum_gen", mutates_args=())
+def latest_k_sum_gen(tokens: Optional[Tensor], history: Optional[Tensor],
+                     write_logits: Optional[Tensor], read_logits: Optional[Tensor],
+                     payloads: Tensor, write_mask: Optional[Tensor], n_literal: int, bos: int,
+                     n_learned: int, ncb: int, cbs: int, position: int, address_space: int,
+                     k: int, want_src: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    lib = nat.library()
+    B, T, C, D = payloads.shape
+    dev = payloads.device
+    values = payloads.new_empty(B, T, C, k, D)
+    mask = torch.empty(B, T, C, k, dtype=torch.bool, device=dev)
+    src = torch.empty((B, T, C, k) if want_src else (0,), dtype=torch.int32, device=dev)
+    out = payloads.new_empty(B, T, C, D)
+    smask = torch.empty(B, T, C, dtype=torch.bool, device=dev)
+    code = nat.payload_code(payloads.dtype)
+    w, r = _descs(tokens, history, write_logits, read_logits, n_literal, bos, n_learned, ncb, cbs,
+                  position)
+    nbytes = lib.ravel_em_latest_k_sum_workspace(B, T, C, D, address_space, k, int(r is not None),
+                                                 int(write_mask is not None), int(want_src), code)
+    ws = nat.workspace(nbytes, dev)
+    nat.check(lib.ravel_em_latest_k_sum_fwd(
+        nat.ref(w), nat.ref(r), nat.ADDR_GEN, nat.ptr(write_mask), nat.ptr(payloads), code,
+        B, T, C, D, address_space, k, nat.ptr(values), nat.ptr(mask),
+        nat.ptr(src) if want_src else None, nat.ptr(out), nat.ptr(smask), nat.ptr(ws), ws.numel(),
+        nat.stream_of(payloads)))
+    nat.after_call(ws)
+    return values, mask, src, out, smask
+
+
+@latest_k_sum_gen.register_fake
+def _latest_k_sum_gen_fake(tokens, history, write_logits, read_logits, payloads, write_mask,
+                           n_literal, bos, n_learned, ncb, cbs, position, address_space, k,
+                           want_src):
+    B, T, C, D = payloads.shape
+    dev = payloads.device
+    return (payloads.new_empty(B, T, C, k, D),
+            torch.empty(B, T, C, k, dtype=torch.bool, device=dev),
+            torch.empty((B, T, C, k) if want_src else (0,), dtype=torch.int32, device=dev),
+            payloads.new_empty(B, T, C, D),
+            torch.empty(B, T, C, dtype=torch.bool, device=dev))
+
+
+def _latest_k_sum_gen_setup(ctx, inputs, output):
+    tokens, history, write_logits, read_logits, _payloads, write_mask = inputs[:6]
+    _, mask, src, _, smask = output
+    ctx.save_for_backward(src, tokens, history, write_logits, read_logits, write_mask)
+    ctx.chain = read_logits is None and write_mask is None
+    ctx.want_src = inputs[-1]
+    ctx.cfg = inputs[6:13]
+    ctx.mark_non_differentiable(mask, src, smask)
+
+
+def _latest_k_sum_gen_grad(ctx, grad_values, _grad_mask, _grad_src, grad_sum, _grad_smask):
+    src, tokens, history, write_logits, read_logits, write_mask = ctx.saved_tensors
+    if not ctx.want_src:
+        raise RuntimeError("ravel_em.latest_k_sum_gen was called without sources; "
+                           "cannot differentiate")
+    grad_payload = _ops.latest_k_backward(src, grad_values, ctx.chain)
+    grad_payload = grad_payload + seg_sum_gen_backward(tokens, history, write_logits, read_logits,
+                                                       write_mask, grad_sum, *ctx.cfg)
+    return (None, None, None, None, grad_payload) + (None,) * 10
+
+
+latest_k_sum_gen.register_autograd(_latest_k_sum_gen_grad, setup_context=_latest_k_sum_gen_setup)
+
+
 # ------------------------------------------------------------ lookups --
 
 
@@ -441,6 +507,25 @@ def sum_lookup(src: LayerAddresses, payloads: Tensor, *, address_space: int,
     m = None if write_mask is None else write_mask.bool().contiguous()
     return seg_sum_gen(tok, hist, wl, rl, payloads.contiguous(), m, *src.cfg(),
                        int(address_space))
+
+
+def last_k_and_sum_lookup(src: LayerAddresses, payloads: Tensor, *, address_space: int,
+                          k: int = 1, write_mask: Optional[Tensor] = None
+                          ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """causal_last_k_and_sum_lookup with the addresses of `src` produced in the
+    kernels; returns (values, mask, summed, sum_mask)."""
+    _check_payloads(src, payloads, write_mask)
+    if k <= 0:
+        raise ValueError("k must be positive")
+    _check_space(address_space)
+    tok, hist, wl, rl = src.tensors()
+    nat.require_device(payloads, tok, hist, wl, rl, write_mask)
+    m = None if write_mask is None else write_mask.bool().contiguous()
+    want_src = torch.is_grad_enabled() and payloads.requires_grad
+    values, mask, _, summed, sum_mask = latest_k_sum_gen(
+        tok, hist, wl, rl, payloads.contiguous(), m, *src.cfg(), int(address_space), int(k),
+        bool(want_src))
+    return values, mask, summed, sum_mask
 
 
 def cache_step(src: LayerAddresses, values: Tensor, filled: Tensor, payloads: Tensor,

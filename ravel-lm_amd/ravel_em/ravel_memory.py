@@ -20,7 +20,7 @@ import torch
 
 from . import _native as nat
 from . import _ops
-from .addressing import LayerAddresses, last_k_lookup, sum_lookup
+from .addressing import LayerAddresses, last_k_and_sum_lookup, last_k_lookup, sum_lookup
 from .addressing import cache_step as _addr_cache_step
 
 Tensor = torch.Tensor
@@ -207,6 +207,58 @@ def causal_sum_lookup(
     graph = torch.is_grad_enabled() and p.requires_grad
     op = _ops.seg_sum_impl if not graph and _ops.eager(w, p, r, m) else _ops.seg_sum
     return op(w, p, r, m, int(address_space))
+
+
+def causal_last_k_and_sum_lookup(
+    write_addresses: Tensor,
+    payloads: Tensor,
+    read_addresses: Optional[Tensor] = None,
+    *,
+    address_space: int,
+    k: int = 1,
+    write_mask: Optional[Tensor] = None,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """``causal_last_k_lookup`` and ``causal_sum_lookup`` of one tape in one call.
+
+    Returns ``(values, mask, summed, sum_mask)``: exactly the results of
+    ``causal_last_k_lookup(write_addresses, payloads, read_addresses,
+    address_space=address_space, k=k, write_mask=write_mask)`` followed by
+    ``causal_sum_lookup(...)`` of the same tape, which is the pair of calls the
+    reference memory layer makes when ``use_sum_read`` is set
+    (ravel_lm/model.py:366-386; each call sorts the tape,
+    ravel_lm/ravel_memory.py:151 and :216).  Here the tape is sorted once for
+    both where one kernel can emit both results.  ``write_addresses`` may be a
+    LayerAddresses, as in causal_last_k_lookup.
+    """
+    if isinstance(write_addresses, LayerAddresses):
+        _no_read(read_addresses)
+        return last_k_and_sum_lookup(write_addresses, payloads, address_space=address_space, k=k,
+                                     write_mask=write_mask)
+    same = read_addresses is None or read_addresses is write_addresses
+    if read_addresses is None:
+        read_addresses = write_addresses
+    if write_addresses.shape != read_addresses.shape:
+        raise ValueError("write_addresses and read_addresses must have the same shape")
+    if write_addresses.ndim != 3:
+        raise ValueError("addresses must have shape [B, T, C]")
+    if payloads.ndim != 4:
+        raise ValueError("payloads must have shape [B, T, C, D]")
+    B, T, C = write_addresses.shape
+    if payloads.shape[:3] != (B, T, C):
+        raise ValueError("payloads leading dimensions must match addresses")
+    if k <= 0:
+        raise ValueError("k must be positive")
+    if write_mask is not None and write_mask.shape != (B, T):
+        raise ValueError("write_mask must have shape [B, T]")
+    nat.require_device(write_addresses, payloads, read_addresses, write_mask)
+    key_dtype = _composite_key_dtype(B, T, C, address_space)
+    w, r = _prepare(write_addresses, None if same else read_addresses, key_dtype)
+    m = None if write_mask is None else write_mask.bool().contiguous()
+    p = payloads.contiguous()
+    graph = torch.is_grad_enabled() and p.requires_grad
+    op = _ops.latest_k_sum_impl if not graph and _ops.eager(w, p, r, m) else _ops.latest_k_sum
+    values, mask, _, summed, sum_mask = op(w, p, r, m, int(address_space), int(k), graph)
+    return values, mask, summed, sum_mask
 
 
 def sort_order(

@@ -5,6 +5,9 @@ line per measurement:
 
   latest_k   causal_last_k_lookup on the config's tape
   seg_sum    causal_sum_lookup on the same tape
+  latest_k_sum  causal_last_k_and_sum_lookup: both on the same tape in one
+             call (the memory layer's pair with use_sum_read); its bytes are
+             the latest-k call's plus the sum rows and mask written
   prefill    RavelLayerCache.prefill of the cfg5 decode cache
   decode     cfg5 RavelLayerCache.step, eager and replayed from a HIP graph
   *_from_*   the memory layer's address production and lookup together
@@ -29,7 +32,8 @@ from typing import Callable, List, Optional
 import torch
 
 from . import workloads
-from .ravel_memory import RavelLayerCache, causal_last_k_lookup, causal_sum_lookup
+from .ravel_memory import (RavelLayerCache, causal_last_k_and_sum_lookup, causal_last_k_lookup,
+                           causal_sum_lookup)
 
 PEAK_GBPS = 8000.0
 
@@ -60,9 +64,18 @@ def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) ->
 
 
 def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None,
-               ops=("latest_k", "seg_sum")) -> List[dict]:
+               ops=("latest_k", "seg_sum", "latest_k_sum")) -> List[dict]:
     B, T, C, D = w.shape
     lines = []
+    if "latest_k_sum" in ops:
+        us = statistics.median(time_calls(
+            lambda: causal_last_k_and_sum_lookup(w.write, w.payload, w.read,
+                                                 address_space=w.address_space, k=w.k),
+            iters=iters))
+        lines.append(_line(w.name, "latest_k_sum", us, workloads.algorithmic_bytes_latest_k_sum(w),
+                           B * T, shape=[B, T, C, D], k=w.k, A=w.address_space,
+                           dtype=str(w.payload.dtype).split(".")[-1],
+                           read="separate" if w.read is not None else "same"))
     if "latest_k" in ops:
         us = statistics.median(time_calls(
             lambda: causal_last_k_lookup(w.write, w.payload, w.read, address_space=w.address_space, k=w.k),
@@ -335,7 +348,7 @@ PARTS = ("tapes", "addresses", "decode", "fused")
 
 
 TAPE_CONFIGS = ("cfg1", "cfg1b", "cfg2_float32", "cfg2_bfloat16", "cfg3", "cfg4", "cfg4_adv")
-TAPE_OPS = ("latest_k", "seg_sum")
+TAPE_OPS = ("latest_k", "seg_sum", "latest_k_sum")
 
 
 def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,

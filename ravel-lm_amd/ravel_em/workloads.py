@@ -232,3 +232,9 @@ def algorithmic_bytes_sum(w: Workload) -> int:
     B, T, C, D = w.shape
     N = B * T * C
     return N * D * w.payload.element_size() + N
+
+
+def algorithmic_bytes_latest_k_sum(w: Workload) -> int:
+    """Latest-k and segmented sum of one tape: inputs read once, both outputs
+    written once (the "latest-k + sum" bytes of the benchmark statement)."""
+    return algorithmic_bytes_latest_k(w) + algorithmic_bytes_sum(w)

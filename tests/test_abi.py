@@ -37,7 +37,18 @@ def test_binding_table_matches_header():
 
 
 def test_abi_version():
-    assert nat.library().ravel_em_abi_version() == 3
+    assert nat.library().ravel_em_abi_version() == 4
+
+
+def test_static_scratch_rejects_oversized_lookups_without_a_device():
+    """The no-allocation entry point checks the size before any HIP call, so a
+    lookup beyond its static scratch fails here, on a host without a GPU."""
+    lib = nat.library()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the size check comes first
+    rc = lib.ravel_em_latest_k_fwd_static(fake, None, nat.INT64, None, fake, nat.BFLOAT16,
+                                          16, 65536, 16, 64, 65536, 1, fake, fake, None, None, None)
+    assert rc == 1  # RAVEL_EM_EINVAL
+    assert "static scratch" in _err()
 
 
 def test_status_query_rejects_bad_arguments_without_a_device():

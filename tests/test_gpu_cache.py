@@ -159,3 +159,26 @@ def test_cfg5_full_size(device):
     assert torch.equal(cache.filled.cpu(), of)
     assert torch.equal(cache.values.cpu(), ov)
     print("[cfg5 full] final cache matches the replay", flush=True)
+
+
+@pytest.mark.parametrize("B,C", [(0, 4), (3, 0)])
+def test_prefill_without_streams_clears_status(device, B, C):
+    """A prefill with no streams launches no sort, yet leaves a clear status word
+    in a workspace that held garbage (and the Python call passes its check)."""
+    from ravel_em import _native as nat
+
+    lib = nat.library()
+    T, A, D, k = 5, 7, 8, 2
+    w = torch.zeros(B, T, C, dtype=torch.long, device=device)
+    p = torch.zeros(B, T, C, D, dtype=torch.bfloat16, device=device)
+    vals = torch.empty(B, C, A, k, D, dtype=torch.bfloat16, device=device)
+    filled = torch.empty(B, C, A, k, dtype=torch.bool, device=device)
+    nbytes = lib.ravel_em_cache_prefill_workspace(B, T, C, A, 0)
+    ws = torch.full((max(int(nbytes), 256),), 0xFF, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    nat.check(lib.ravel_em_cache_prefill(w.data_ptr(), nat.INT64, None, p.data_ptr(), nat.BFLOAT16,
+                                         B, T, C, D, A, k, vals.data_ptr(), filled.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), stream))
+    assert nat.status_word(ws) == 0
+    cache = RavelLayerCache.prefill(w, p, address_space=A, k=k)
+    assert cache.values.shape == (B, C, A, k, D)

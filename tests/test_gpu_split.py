@@ -121,6 +121,9 @@ def test_gradients_split(device, sep, masked):
         (g_sum,) = torch.autograd.grad(sums, x, gs)
         return g_lk, g_sum
 
+    # the forward calls split; the backward nodes run on autograd's worker
+    # thread, outside this thread's range size (test_backward_entry_points_split
+    # splits those)
     with split_slots(2 * T * C * k):  # latest-k: two rows per range; sums: six
         g_lk, g_sum = grads()
     with split_slots(T * C):  # one row per range for both
@@ -136,6 +139,61 @@ def test_gradients_split(device, sep, masked):
     truth, _, _ = oracle.seg_sum_grad(host[0], gs.cpu().double(), host[2], address_space=A,
                                    write_mask=host[3])
     for g in (g_sum, g_sum1):
+        assert torch.allclose(g.cpu().double(), truth, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("sep,masked", [(False, False), (True, False), (False, True)])
+def test_backward_entry_points_split(device, sep, masked):
+    """The two backward entry points split into ranges.  The range size is set
+    per thread and autograd runs backward nodes on its own worker thread, so
+    test_gradients_split splits the forward calls only; here the backward C
+    entry points are called on this thread, unsplit and in one-row ranges, and
+    checked against each other and the oracle (latest-k: the sorted form, whose
+    sources are made range-local and back; sums: the reverse walk)."""
+    B, T, C, A, k, D = 5, 300, 2, 7, 3, 8
+    w, p, r, m, host = tape(device, B, T, C, A, read=sep, mask=masked, D=D, seed=14)
+    print(f"[split] backward entry points sep={sep} mask={masked}", flush=True)
+    lib = nat.library()
+    code = nat.FLOAT32
+    stream = nat.stream_of(p)
+    _, _, src = causal_last_k_sources(w, p, r, address_space=A, k=k, write_mask=m)
+    gv = torch.randn(B, T, C, k, D, generator=torch.Generator().manual_seed(15)).to(device)
+    gs = torch.randn(B, T, C, D, generator=torch.Generator().manual_seed(16)).to(device)
+
+    def lk_bwd():
+        out = torch.empty(B, T, C, D, device=device)
+        ws = nat.workspace(lib.ravel_em_latest_k_bwd_workspace(B, T, C, D, k, code, 0), device)
+        nat.check(lib.ravel_em_latest_k_bwd(src.data_ptr(), gv.data_ptr(), code, B, T, C, D, k, 0,
+                                            out.data_ptr(), ws.data_ptr(), ws.numel(), stream))
+        assert nat.status_word(ws) == 0
+        return out
+
+    def sum_bwd():
+        out = torch.empty(B, T, C, D, device=device)
+        ws = nat.workspace(lib.ravel_em_seg_sum_bwd_workspace(B, T, C, D, A, int(sep), int(masked),
+                                                              code), device)
+        nat.check(lib.ravel_em_seg_sum_bwd(w.data_ptr(), nat.ptr(r), nat.INT64, nat.ptr(m),
+                                           gs.data_ptr(), code, B, T, C, D, A, out.data_ptr(),
+                                           ws.data_ptr(), ws.numel(), stream))
+        assert nat.status_word(ws) == 0
+        return out
+
+    base_lk, base_sum = lk_bwd(), sum_bwd()
+    with split_slots(T * C * k):  # one batch row per range
+        lk1 = lk_bwd()
+    with split_slots(T * C):
+        sum1 = sum_bwd()
+    # each source's slots lie in its own row, so the slot-order sums are unchanged
+    assert torch.equal(lk1, base_lk)
+    want = torch.zeros(B * T * C, D, dtype=torch.float64)
+    osrc = oracle.latest_k_src(host[0], host[2], address_space=A, k=k, write_mask=host[3])
+    sel = osrc.reshape(-1) >= 0
+    want.index_add_(0, torch.from_numpy(osrc.reshape(-1)[sel]),
+                    gv.cpu().double().reshape(-1, D)[torch.from_numpy(sel)])
+    assert torch.allclose(lk1.cpu().double().reshape(-1, D), want, rtol=1e-5, atol=1e-5)
+    truth, _, _ = oracle.seg_sum_grad(host[0], gs.cpu().double(), host[2], address_space=A,
+                                      write_mask=host[3])
+    for g in (base_sum, sum1):
         assert torch.allclose(g.cpu().double(), truth, rtol=1e-5, atol=1e-5)
 
 
