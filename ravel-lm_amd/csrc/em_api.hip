@@ -577,8 +577,7 @@ size_t sum_ws_t(const Tape& tp, int64_t D, int dtype, bool direct, bool backward
 // The latest-k lookup and the segmented sum of one tape (the pair of calls of
 // ravel_lm/model.py:366-386) over one sort:
 //   short tapes: the merged sum kernel, whose LDS sort already orders reads
-//     and writes, also writes every read's latest-k sources; one gather makes
-//     the values;
+//     and writes, also writes every read's latest-k rows (one launch);
 //   long tapes, reads = writes, k = 1: one full sort, then the walker's sum
 //     walk also stores each record's predecessor row (the latest-1 value);
 //   otherwise: the two operators one after the other on the same workspace,
@@ -600,11 +599,10 @@ int latest_k_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
   const int64_t row_bytes = D * dtype_size(dtype);
   Tape tp = tape;
   if (seg_sum_merged_applies(tp, D, dtype, payload, out_sum) &&
-      seg_sum_merged_sources_apply(tp, D, dtype, k)) {
+      seg_sum_merged_values_apply(tp, D, dtype, k) && ((uintptr_t)out_values & 15) == 0) {
     Bump bp(ws);
-    SortWs<U> sw = take_sort<U>(bp, tp);
+    SortWs<U> sw = take_sort<U>(bp, tp);  // key buffers hold produced addresses
     tp.status = sw.status;
-    int32_t* src = out_src ? out_src : bp.take<int32_t>((size_t)(tp.n() * k));
     if (int rc = check_ws(bp, wsb)) return rc;
     stage_begin(kStageSum, s);
     AddrIn wd, rd;
@@ -612,15 +610,9 @@ int latest_k_sum_run(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
     if (e == hipSuccess && ra) e = compact_addresses(*ra, tp, sw.ka, &rd, s);
     if (e == hipSuccess)
       e = seg_sum_merged(wd, ra ? &rd : nullptr, wmask, payload, dtype, tp, D, out_sum,
-                         out_sum_mask, s, src, k);
+                         out_sum_mask, s, k, out_values, out_mask, out_src);
     stage_end(kStageSum, s);
-    if (e != hipSuccess) return hip_fail(e, "segmented sum and sources");
-    stage_begin(kStageGather, s);
-    // reads = writes and k == 1: every record is the source of at most one slot
-    e = gather_rows(payload, tp.n(), src, tp.n() * k, row_bytes, out_values, out_mask, s,
-                    !ra && k == 1);
-    stage_end(kStageGather, s);
-    if (e != hipSuccess) return hip_fail(e, "gather");
+    if (e != hipSuccess) return hip_fail(e, "segmented sum and latest-k");
     return RAVEL_EM_OK;
   }
   if (!ra && !wmask && k == 1 && seg_sum_joint_applies(tp, D, dtype, payload, out_sum, out_values)) {

@@ -312,13 +312,14 @@ hipError_t seg_sum(const U* sorted, const void* payload, int dtype, const Tape& 
 // (ra null = reads at the write addresses), rows of whole 16-byte units.
 bool seg_sum_merged_applies(const Tape& tp, int64_t D, int dtype, const void* payload,
                             const void* out);
-// With osrc, the same launch also writes every read's latest-k sources
-// (record-major [B,T,C,k] int32, -1 for an empty slot) when
-// seg_sum_merged_sources_apply holds (k <= 8).
-bool seg_sum_merged_sources_apply(const Tape& tp, int64_t D, int dtype, int64_t k);
+// With vout, the same launch is also the latest-k lookup of the tape when
+// seg_sum_merged_values_apply holds (k <= 8): vout [B,T,C,k,D] values, vmask
+// [B,T,C,k] and, with osrc, the int32 sources [B,T,C,k] (-1 for an empty slot).
+bool seg_sum_merged_values_apply(const Tape& tp, int64_t D, int dtype, int64_t k);
 hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                           const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
-                          uint8_t* omask, hipStream_t s, int32_t* osrc = nullptr, int64_t k = 0);
+                          uint8_t* omask, hipStream_t s, int64_t k = 0, void* vout = nullptr,
+                          uint8_t* vmask = nullptr, int32_t* osrc = nullptr);
 // Forward sums and latest-1 lookup of reads = writes over one sorted tape in
 // one walker launch (seg_sum_joint_applies: rows of 1..64 16-byte units, a
 // power of two; 16-byte aligned rows): out_sum/omask as seg_sum's direct form,
@@ -371,6 +372,7 @@ template <typename U>
 hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, int64_t k,
                          int64_t row_bytes, void* values, uint8_t* filled, hipStream_t s);
 hipError_t fill_bytes(void* dst, uint8_t value, size_t bytes, hipStream_t s);
+hipError_t copy_bytes(void* dst, const void* src, size_t bytes, hipStream_t s);
 
 // dtype codes shared with the C ABI header.
 enum Dtype : int {

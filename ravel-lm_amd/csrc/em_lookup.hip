@@ -662,7 +662,37 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ p, int6
   for (int64_t i = tid; i < rest; i += stride) p[i < head ? i : i + body * 16] = v;
 }
 
+// Copy of n bytes: where source and destination share their 16-byte
+// alignment, the aligned body in 16-byte units, the head and tail byte by
+// byte (everything byte by byte otherwise).
+__global__ __launch_bounds__(256) void copy_kernel(uint8_t* __restrict__ d,
+                                                   const uint8_t* __restrict__ p, int64_t n,
+                                                   int64_t head, int64_t body) {
+  const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const u32x4* q = (const u32x4*)(p + head);
+  u32x4* o = (u32x4*)(d + head);
+  for (int64_t i = tid; i < body; i += stride) o[i] = q[i];
+  const int64_t rest = n - body * 16;  // head + tail bytes
+  for (int64_t i = tid; i < rest; i += stride) {
+    const int64_t j = i < head ? i : i + body * 16;
+    d[j] = p[j];
+  }
+}
+
 }  // namespace
+
+hipError_t copy_bytes(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  const int64_t n = (int64_t)bytes;
+  const bool same = (((uintptr_t)dst ^ (uintptr_t)src) & 15) == 0;
+  int64_t head = same ? (int64_t)((16 - ((uintptr_t)dst & 15)) & 15) : n;
+  if (head > n) head = n;
+  const int64_t body = (n - head) / 16;
+  copy_kernel<<<grid_for(body > 0 ? body : (n + 255) / 256, 256), 256, 0, s>>>(
+      (uint8_t*)dst, (const uint8_t*)src, n, head, body);
+  return hipGetLastError();
+}
 
 int dtype_size(int dtype) {
   switch (dtype) {

@@ -388,9 +388,9 @@ __device__ __forceinline__ void add_unit(Acc* acc, u32x4 x) {
 // VAL (the fast form, reads = writes): the final walk also writes every
 // record's latest-1 value, the row of the position before it in its run (the
 // row the walk has just added; +0.0 at a run start), into vout at the sum's
-// offset, the same mask byte into vmask and, with vsrc, that row's record id
-// (-1 at a run start): the latest-1 lookup of the same sorted tape with no
-// sort, link or gather of its own.
+// offset, with vmask the same mask byte into vmask and, with vsrc, that row's
+// record id (-1 at a run start): the latest-1 lookup of the same sorted tape
+// with no sort, link or gather of its own.
 template <typename U, typename XIn, typename XOut, typename Acc, typename LoadF, typename StoreF,
           bool REV, bool IN_SORTED, bool INCL, bool OUT_SORTED, bool WMASK, bool RT, bool FAST,
           bool VAL = false>
@@ -651,7 +651,8 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
       const __amdgpu_buffer_rsrc_t mrs =
           __builtin_amdgcn_make_buffer_rsrc((void*)(omask + vbase), 0, (int)(T * C), kRsrcWord3);
       const __amdgpu_buffer_rsrc_t vmrs = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(VAL ? vmask + vbase : vmask), 0, VAL ? (int)(T * C) : 0, kRsrcWord3);
+          (void*)(VAL && vmask ? vmask + vbase : vmask), 0, VAL && vmask ? (int)(T * C) : 0,
+          kRsrcWord3);
       const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(VAL && vsrc ? vsrc + vbase : vsrc), 0, VAL && vsrc ? (int)(T * C * 4) : 0,
           kRsrcWord3);
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
         const uint32_t moff = (k & kCodeTime) * (uint32_t)C;
         __builtin_amdgcn_raw_buffer_store_b8(has, mrs, moff, 0, 0);
         if (VAL) {
-          __builtin_amdgcn_raw_buffer_store_b8(has, vmrs, moff, 0, 0);
+          if (vmask) __builtin_amdgcn_raw_buffer_store_b8(has, vmrs, moff, 0, 0);
           if (vsrc) {
             const uint32_t pt = i > 0 ? (cw[i - 1] & kCodeTime) : s_ptime;
             const int32_t sr = has ? vbase + (int32_t)pt * Ci : -1;
@@ -722,10 +723,12 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 //      a fold over the walkers, then the walk): writes add their payload row,
 //      each read stores the running sum and the mask (some write before it).
 // So the prefix rows are never stored and re-read, and reads need no search.
-// With KS > 0 the walk also emits every read's latest-k sources (k <= KS): each
-// walker keeps the times of the last KS writes of its run in registers, newest
-// first, and a read stores k record ids (-1 past the run's writes), the
-// search of ravel_memory.py:159-168 without a search.
+// With KS > 0 the walk is also the latest-k lookup (k <= KS) of the same tape:
+// each walker keeps the times and payload rows of the last KS writes of its
+// run in registers, newest first, and a read stores its k slot rows (+0.0 past
+// the run's writes) straight into the values output, their mask bytes and,
+// when wanted, the slots' record ids: the searchsorted and gather of
+// ravel_memory.py:159-176 without a search, a source array or a gather.
 constexpr int kMergedThreads = 512;  // two blocks per CU (LDS and registers)
 constexpr int kMergedItems = 8192;  // 2T
 constexpr int kMergedLr = 4096;     // addresses of the last-read table
@@ -808,15 +811,16 @@ __device__ __forceinline__ int64_t addr_col_value(const AddrCol& col, uint32_t t
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Sources of one read: slot j < min(k, cnt) is record ring[j], the others -1;
-// k int32 words at byte `off` of the rsrc (an offset at or past 2^30 stores
-// nothing).  k == KS stores whole vectors.
+// Sources of one read: slot j < min(k, cnt) is record rbase + ring[j] * C
+// (ring[j] a time), the others -1; k int32 words at byte `off` of the rsrc (an
+// offset at or past 2^30 stores nothing).  k == KS stores whole vectors.
 template <int KS>
 __device__ __forceinline__ void store_sources(__amdgpu_buffer_rsrc_t rs, uint32_t off,
-                                              const uint32_t* ring, int cnt, int k) {
+                                              const uint32_t* ring, int cnt, int k,
+                                              int32_t rbase, int32_t Ci) {
   int32_t v[KS];
 #pragma unroll
-  for (int j = 0; j < KS; ++j) v[j] = j < cnt ? (int32_t)ring[j] : -1;
+  for (int j = 0; j < KS; ++j) v[j] = j < cnt ? rbase + (int32_t)ring[j] * Ci : -1;
   if (KS == 1 || k == KS) {
     if constexpr (KS == 1) {
       __builtin_amdgcn_raw_buffer_store_b32((uint32_t)v[0], rs, off, 0, 0);
@@ -844,7 +848,8 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     int npass, int G, int64_t nseg, const XIn* __restrict__ payload,
     XIn* __restrict__ out, uint8_t* __restrict__ omask, uint32_t* __restrict__ status,
     uint32_t* __restrict__ gate, uint32_t tag, uint32_t gate_lo, uint32_t gate_hi,
-    uint32_t gate_target, uint32_t gate_ticks, int32_t* __restrict__ osrc, int kslots) {
+    uint32_t gate_target, uint32_t gate_ticks, int kslots, XIn* __restrict__ vout,
+    uint8_t* __restrict__ vmask, int32_t* __restrict__ osrc, int vtemp) {
   constexpr int NT = kMergedThreads;
   constexpr int NWV = NT / kWave;
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
@@ -852,8 +857,8 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   static_assert(NT * CPU * sizeof(Acc) + NT * sizeof(Acc) <= kMergedMaskOff,
                 "walker tails and group sums stay below the mask bytes");
   // walk batch: 16 items, 8 with fp64 sums (their conversions need the
-  // registers that a wider batch would take)
-  constexpr int WB = sizeof(Acc) == sizeof(float) ? 16 : 8;
+  // registers that a wider batch would take) or rings of rows
+  constexpr int WB = sizeof(Acc) == sizeof(float) && KS == 0 ? 16 : 8;
   __shared__ __align__(16) uint32_t keys[kMergedItems];
   __shared__ __align__(16) unsigned char un[kMergedUnion];
   __shared__ uint32_t dstart[kRankRadix];
@@ -1013,22 +1018,34 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   uint8_t* hm = (uint8_t*)(un + kMergedMaskOff);
   Acc acc[CPU];
   bool hasw = false;
-  // KS > 0: the record ids of the run's last KS writes (ring[0] the newest)
-  // and how many of them belong to the run; the sources of a read (k int32
-  // words, record-major) leave from lane v == 0 of its walker.  Pads count as
-  // writes here; they only ever stand before a run start or after the walk's
-  // items.
+  // KS > 0: the times of the run's last KS writes (ring[0] the newest), how
+  // many of them belong to the run (rcnt, at most KS) and, in the final walk,
+  // this lane's unit of their payload rows (vring).  A read stores its k slot
+  // rows (value row j of record r at byte (r k + j) G 16 of vout), keeps the
+  // count for its mask bytes in hm and, with osrc, stores the slots' record
+  // ids from lane v == 0.  rcnt > 0 exactly when the read's sum has a term.
+  // Pads count as writes here; they only ever stand before a run start or
+  // after the walk's items.
   constexpr int KR = KS > 0 ? KS : 1;
   uint32_t ring[KR];
+  u32x4 vring[KR];
   int rcnt = 0;
 #pragma unroll
-  for (int j = 0; j < KR; ++j) ring[j] = 0u;
+  for (int j = 0; j < KR; ++j) {
+    ring[j] = 0u;
+    vring[j] = u32x4{0u, 0u, 0u, 0u};
+  }
   const int32_t rbase32 = (int32_t)rbase, Ci = (int32_t)C;
-  const uint32_t sstride = (uint32_t)(C * kslots * 4);
+  const uint32_t sstride = (uint32_t)(C * kslots * 4);  // sources of one time step
+  const uint32_t vstride = tstride * (uint32_t)kslots;  // value rows of one time step
+  const uint32_t rowb = (uint32_t)G * 16u;
   const uint32_t slane = v == 0 ? 0u : 0x80000000u;
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(osrc ? osrc + rbase * kslots : osrc), 0, KS > 0 ? (int)(T * sstride) : 0,
+      (void*)(osrc ? osrc + rbase * kslots : osrc), 0, KS > 0 && osrc ? (int)(T * sstride) : 0,
       kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(KS > 0 ? (unsigned char*)vout + rbase * kslots * (int64_t)rowb : (unsigned char*)vout),
+      0, KS > 0 ? (int)(T * vstride) : 0, kRsrcWord3);
   // Items [from, to), in whole batches from the one holding `from` (items
   // outside are pads): a run start resets the sum and the has-a-write flag, a
   // loaded write adds its row, a read (STORE) stores the sum and the flag.
@@ -1038,8 +1055,8 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     constexpr bool STORE = decltype(store_tag)::value;
     constexpr int aux = STORE ? kBufNontemporal : 0;
     constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
-    for (int i0 = from & ~(WB - 1); i0 < to; i0 += WB) {
-      uint32_t cw[WB];
+    // the code words of batch i0 and their rows (every load in flight)
+    auto fetch = [&](int i0, uint32_t* cw, u32x4* x) {
 #pragma unroll
       for (int q = 0; q < WB / 4; ++q) {
         const u32x4 c4 = *(const u32x4*)&keys[i0 + 4 * q];
@@ -1048,11 +1065,12 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int m = 0; m < WB; ++m)
         if (i0 + m < from || i0 + m >= to) cw[m] = kPad;
-      u32x4 x[WB];
 #pragma unroll
       for (int m = 0; m < WB; ++m)
         x[m] = __builtin_amdgcn_raw_buffer_load_b128(
             prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad), 0, aux);
+    };
+    auto process = [&](const uint32_t* cw, const u32x4* x) {
 #pragma unroll
       for (int m = 0; m < WB; ++m) {
         const uint32_t k = cw[m];
@@ -1060,28 +1078,56 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int j = 0; j < CPU; ++j) acc[j] = st ? Acc(0) : acc[j];
         hasw = hasw && !st;
+        rcnt = st ? 0 : rcnt;
         if (STORE) {
           const uint32_t ns = k & kCodeNoStore;
+          // with KS > 0 the sums share the write stream with k times their
+          // bytes of value rows and skip the caches; alone they go through L2
           __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XIn, StoreF, Acc, CPU>(acc), ors,
-                                                 (__umul24(k, tstride) + v16) | ns, 0, 0);
-          hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = hasw ? 1 : 0;
+                                                 (__umul24(k, tstride) + v16) | ns, 0,
+                                                 KS > 0 ? kBufNontemporal : 0);
+          hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = KS > 0 ? (uint8_t)rcnt : (hasw ? 1 : 0);
         }
         if constexpr (KS > 0) {
-          rcnt = st ? 0 : rcnt;
-          const bool wr = k & kCodeNoStore;
-          if (STORE)
-            store_sources<KS>(srs, (__umul24(k, sstride) | (k & kCodeNoStore)) | slane, ring, rcnt,
-                              kslots);
+          const uint32_t ns = k & kCodeNoStore;  // a write: it stores nothing, it enters the ring
+          const bool wr = ns != 0;
+          if (STORE) {
+            const uint32_t vo = __umul24(k, vstride) | ns;
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            // value rows of small tapes stay in the caches, larger ones stream
+#pragma unroll
+            for (int j = 0; j < KR; ++j) {
+              const u32x4 val = j < rcnt ? vring[j] : z;
+              const uint32_t off = (vo + (uint32_t)j * rowb + v16) | (j < kslots ? 0u : 0x80000000u);
+              if (vtemp)
+                __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, 0);
+              else
+                __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, kBufNontemporal);
+            }
+            if (osrc)
+              store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, ring, rcnt, kslots,
+                                rbase32, Ci);
+#pragma unroll
+            for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
+            vring[0] = wr ? x[m] : vring[0];
+          }
 #pragma unroll
           for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
-          ring[0] = wr ? (uint32_t)(rbase32 + (int32_t)__umul24(k, (uint32_t)Ci)) : ring[0];
+          ring[0] = wr ? (k & kCodeTime) : ring[0];
           rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
         }
         add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
         hasw = hasw || !(k & kCodeNoLoad);
       }
+    };
+    for (int i0 = from & ~(WB - 1); i0 < to; i0 += WB) {
+      uint32_t cw[WB];
+      u32x4 x[WB];
+      fetch(i0, cw, x);
+      process(cw, x);
     }
   };
+
   // Run-aligned ranges: a walker with a run start in its range walks from
   // its first one to the first start of the next walker that has one, so no
   // run crosses walkers, and starts from zero.  When one such range would
@@ -1201,7 +1247,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   if constexpr (KS > 0) {
     // the ring carried into the range: the newest writes of the earlier
     // walkers' tails, back to one that holds a run start (its tail starts
-    // there) or until KS are found
+    // there) or until KS are found; then their rows
     rcnt = 0;
     for (int w2 = w - 1; w2 >= 0 && rcnt < KS; --w2) {
       const int n2w = rc[w2];
@@ -1213,15 +1259,39 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
       rcnt = rcnt + n2w < KS ? rcnt + n2w : KS;
       if (hs[w2]) break;
     }
+#pragma unroll
+    for (int j = 0; j < KR; ++j)
+      vring[j] = __builtin_amdgcn_raw_buffer_load_b128(
+          prs, (__umul24(ring[j], tstride) + v16) | (j < rcnt ? 0u : kCodeNoLoad), 0, 0);
   }
   walk(rs, re, std::true_type{});
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t mrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(omask + rbase), 0, (int)(T * C), kRsrcWord3);
+  // KS > 0: the latest-k mask, k bytes a read (slot j filled when j < count)
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(KS > 0 ? vmask + rbase * kslots : vmask), 0, KS > 0 ? (int)(T * C * kslots) : 0,
+      kRsrcWord3);
 #pragma unroll 1
-  for (int t = tid; t < T; t += NT)
-    __builtin_amdgcn_raw_buffer_store_b8(hm[t], mrs, (uint32_t)t * (uint32_t)C, 0, 0);
+  for (int t = tid; t < T; t += NT) {
+    const uint32_t cnt = hm[t];
+    __builtin_amdgcn_raw_buffer_store_b8(cnt != 0 ? 1 : 0, mrs, (uint32_t)t * (uint32_t)C, 0, 0);
+    if constexpr (KS > 0) {
+      const uint32_t mo = (uint32_t)t * (uint32_t)(C * kslots);
+      // byte j of the little-endian words: slot j's flag
+      const uint64_t bits = 0x0101010101010101ull & ((cnt >= 8 ? ~0ull : (1ull << (8 * cnt)) - 1ull));
+      if (kslots == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)bits, lrs, mo, 0, 0);
+      } else if (kslots == 8) {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)bits, (uint32_t)(bits >> 32)}, lrs,
+                                              mo, 0, 0);
+      } else {
+        for (int j = 0; j < kslots; ++j)
+          __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(bits >> (8 * j)), lrs, mo + (uint32_t)j, 0, 0);
+      }
+    }
+  }
 }
 
 bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, const void* out) {
@@ -1236,17 +1306,23 @@ bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, cons
 // Ring size of the merged kernel's latest-k sources (0: none).
 int merged_ring(int64_t k) { return k < 1 ? 0 : (k == 1 ? 1 : (k <= 4 ? 4 : 8)); }
 
-bool merged_sources_apply(const Tape& tp, int64_t row_bytes, int64_t k) {
+// The merged kernel also makes the latest-k lookup: k <= 8, the walkers'
+// tail rings fit their LDS, and the value rows and sources of a segment sit
+// below 2^30 bytes of its base (value rows of one time step below 2^24).
+bool merged_values_apply(const Tape& tp, int64_t row_bytes, int64_t k) {
   const int64_t NW = kMergedThreads / (row_bytes / 16);
   const int KS = merged_ring(k);
   return k >= 1 && k <= 8 && NW * (KS + 1) * 4 <= kMergedRingBytes &&
-         tp.T * tp.C * k * 4 <= ((int64_t)1 << 30);
+         tp.T * tp.C * k * 4 <= ((int64_t)1 << 30) &&
+         tp.C * k * row_bytes < ((int64_t)1 << 24) &&
+         tp.T * tp.C * k * row_bytes <= ((int64_t)1 << 30);
 }
 
 template <int DT>
 hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                             const void* payload, const Tape& tp, int64_t D, void* out,
-                            uint8_t* omask, int32_t* osrc, int k, hipStream_t s) {
+                            uint8_t* omask, int k, void* vout, uint8_t* vmask, int32_t* osrc,
+                            hipStream_t s) {
   using E = Elem<DT>;
   using S = typename E::store_t;
   using Acc = typename E::acc_t;
@@ -1269,15 +1345,18 @@ hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* w
   segsum_merged_kernel<IT, KS, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                 \
       wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
       tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
-      tag, gate_lo, gate_hi, target, ticks, osrc, k)
+      tag, gate_lo, gate_hi, target, ticks, k, (S*)vout, vmask, osrc, vtemp)
 #define REM_MG_KS(IT)                           \
-  switch (osrc ? merged_ring(k) : 0) {          \
+  switch (vout ? merged_ring(k) : 0) {          \
     case 0: REM_MG(IT, 0); break;               \
     case 1: REM_MG(IT, 1); break;               \
     case 4: REM_MG(IT, 4); break;               \
     default: REM_MG(IT, 8); break;              \
   }
-  if (osrc && !merged_sources_apply(tp, G * 16, k)) return hipErrorInvalidValue;
+  if (vout && (!vmask || !merged_values_apply(tp, G * 16, k))) return hipErrorInvalidValue;
+  // value rows through the caches while they fit the 256 MB last-level cache
+  // twice over (measured faster up to 268 MB; streamed past it)
+  const int vtemp = tp.n() * k * G * 16 <= ((int64_t)512 << 20) ? 1 : 0;
   if (2 * tp.T <= 4 * kMergedThreads) {
     REM_MG_KS(4);
   } else {
@@ -1422,12 +1501,16 @@ hipError_t seg_sum_joint_t(const U* sorted, const void* payload, const Tape& tp,
   const int64_t nparts = (tp.T + kPartPos - 1) / kPartPos;
   const int64_t blocks = tp.nseg() * nparts;
   uint64_t* tickets = walk + seg_sum_status_words(tp, D, sizeof(Acc));
+  // The two masks of latest-1 are the same bytes: the walk stores them once,
+  // at random records, and one sequential copy makes the other.
   segsum_walk_kernel<U, S, S, Acc, E, E, false, false, false, false, true, false, true, true>
       <<<(unsigned)blocks, kWalkThreads, 0, s>>>(sorted, (const S*)payload, tp.T, tp.C, D,
                                                  tp.tbits, (int)G, nparts, (S*)out_sum, omask,
                                                  walk, tickets, tp.status, 0, (S*)out_values,
-                                                 vmask, vsrc);
-  return hipGetLastError();
+                                                 nullptr, vsrc);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return copy_bytes(vmask, omask, (size_t)tp.n(), s);
 }
 
 template <int DT, typename U>
@@ -1518,20 +1601,21 @@ template hipError_t seg_sum_joint<uint64_t>(const uint64_t*, const void*, int, c
                                             int64_t, void*, uint8_t*, void*, uint8_t*, int32_t*,
                                             uint64_t*, hipStream_t);
 
-bool seg_sum_merged_sources_apply(const Tape& tp, int64_t D, int dtype, int64_t k) {
-  return merged_sources_apply(tp, D * dtype_size(dtype), k);
+bool seg_sum_merged_values_apply(const Tape& tp, int64_t D, int dtype, int64_t k) {
+  return merged_values_apply(tp, D * dtype_size(dtype), k);
 }
 
 hipError_t seg_sum_merged(const AddrIn& wa, const AddrIn* ra, const uint8_t* wmask,
                           const void* payload, int dtype, const Tape& tp, int64_t D, void* out,
-                          uint8_t* omask, hipStream_t s, int32_t* osrc, int64_t k) {
+                          uint8_t* omask, hipStream_t s, int64_t k, void* vout, uint8_t* vmask,
+                          int32_t* osrc) {
   if (!tp.status) return hipErrorInvalidValue;
   const int kk = (int)k;
   switch (dtype) {
-    case kF32: return seg_sum_merged_t<kF32>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
-    case kF64: return seg_sum_merged_t<kF64>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
-    case kBF16: return seg_sum_merged_t<kBF16>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
-    case kF16: return seg_sum_merged_t<kF16>(wa, ra, wmask, payload, tp, D, out, omask, osrc, kk, s);
+    case kF32: return seg_sum_merged_t<kF32>(wa, ra, wmask, payload, tp, D, out, omask, kk, vout, vmask, osrc, s);
+    case kF64: return seg_sum_merged_t<kF64>(wa, ra, wmask, payload, tp, D, out, omask, kk, vout, vmask, osrc, s);
+    case kBF16: return seg_sum_merged_t<kBF16>(wa, ra, wmask, payload, tp, D, out, omask, kk, vout, vmask, osrc, s);
+    case kF16: return seg_sum_merged_t<kF16>(wa, ra, wmask, payload, tp, D, out, omask, kk, vout, vmask, osrc, s);
     default: return hipErrorInvalidValue;
   }
 }

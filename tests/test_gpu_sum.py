@@ -166,11 +166,13 @@ def test_sum_integer_payloads_are_exact(device):
     assert torch.equal(out.cpu().double(), truth) and torch.equal(mask.cpu(), tmask)
 
 
-@pytest.mark.parametrize("name", ["cfg1", "cfg2_f32", "cfg2_bf16", "cfg3", "cfg4", "cfg4_adv"])
+@pytest.mark.parametrize("name", ["cfg1", "cfg1b", "cfg2_f32", "cfg2_bf16", "cfg3", "cfg4",
+                                  "cfg4_adv"])
 def test_sum_baseline_configs(device, name):
     print(f"[sum parity] {name}", flush=True)
     w = {
         "cfg1": lambda: workloads.cfg1(device),
+        "cfg1b": lambda: workloads.cfg1(device, variant="1b"),
         "cfg2_f32": lambda: workloads.cfg2(device, torch.float32),
         "cfg2_bf16": lambda: workloads.cfg2(device, torch.bfloat16),
         "cfg3": lambda: workloads.cfg3(device),
