@@ -10,6 +10,16 @@ Reference interface (file:line in the reference tree):
   causal_last_k_lookup   ravel_lm/ravel_memory.py:52-176
   causal_sum_lookup      ravel_lm/ravel_memory.py:179-241
   RavelLayerCache        ravel_lm/ravel_memory.py:244-292
+  causal_last_k_and_sum_lookup  the pair of the two lookups that
+                         ravel_lm/model.py:366-386 makes on one tape
+
+Device-side waits.  The sorts and the long-tape sums coordinate blocks through
+bounded waits; a wait that runs out of spins sets a bit in the call's status
+word instead of hanging, and the call's outputs are then not valid.  The
+functions here do not read that word by default (reading it synchronizes the
+stream): set RAVEL_EM_CHECK_STATUS=1, or call
+ravel_em._native.set_status_check(True), to have every call read it and raise
+DeviceWaitError when a bit is set.  The tests run with the check on.
 """
 from __future__ import annotations
 
