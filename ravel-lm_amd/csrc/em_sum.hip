@@ -723,6 +723,10 @@ __global__ __launch_bounds__(kWalkThreads) void segsum_walk_kernel(
 //      a fold over the walkers, then the walk): writes add their payload row,
 //      each read stores the running sum and the mask (some write before it).
 // So the prefix rows are never stored and re-read, and reads need no search.
+// SAME (reads at the write addresses, no write mask): the read and the write
+// of one time share their address, so only the T write keys a << tbits | t
+// are loaded and sorted (half the sort), and sorted record i becomes the
+// read 2i and the write 2i + 1 of the merged tape.
 // With KS > 0 the walk is also the latest-k lookup (k <= KS) of the same tape:
 // each walker keeps the times and payload rows of the last KS writes of its
 // run in registers, newest first, and a read stores its k slot rows (+0.0 past
@@ -841,7 +845,7 @@ __device__ __forceinline__ void store_sources(__amdgpu_buffer_rsrc_t rs, uint32_
   }
 }
 
-template <int ITEMS, int KS, typename XIn, typename Acc, typename LoadF, typename StoreF>
+template <int ITEMS, int KS, bool SAME, typename XIn, typename Acc, typename LoadF, typename StoreF>
 __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void segsum_merged_kernel(
     const void* __restrict__ waddr, int wkind, const void* __restrict__ raddr, int rkind,
     const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int trunc32, int tbits,
@@ -887,7 +891,28 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   }
   // 1. merged keys (straight to LDS) from the segment's address columns;
   // thread tid takes times tid, tid + NT, ...
-  {
+  if constexpr (SAME) {
+    constexpr int KT = ITEMS / 2;  // times per thread (T <= NT * KT)
+    constexpr int KC = KT < 4 ? KT : 4;  // times per round of loads
+    const AddrCol wc = addr_col(waddr, wkind, b, c, T, C);
+    const bool tr = trunc32 != 0;
+#pragma unroll
+    for (int m0 = 0; m0 < KT; m0 += KC) {
+      uint32_t wl[KC], wh[KC];
+#pragma unroll
+      for (int m = 0; m < KC; ++m) {
+        const uint32_t t = (uint32_t)((m0 + m) * NT + tid);
+        addr_col_load(wc, t, t < (uint32_t)T, &wl[m], &wh[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < KC; ++m) {
+        const uint32_t t = (uint32_t)((m0 + m) * NT + tid);
+        if (t < (uint32_t)T)
+          keys[t] = ((uint32_t)reduce_addr(addr_col_value(wc, t, wl[m], wh[m]), A, kWrap, tr)
+                     << tbits) | t;
+      }
+    }
+  } else {
     constexpr int KT = ITEMS / 2;  // times per thread (T <= NT * KT)
     constexpr int KC = KT < 4 ? KT : 4;  // times per round of loads
     const AddrCol wc = addr_col(waddr, wkind, b, c, T, C);
@@ -931,31 +956,36 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   static_assert(NWV * kRankRadix * (sizeof(uint32_t) + sizeof(uint64_t)) <= kMergedUnion,
                 "counters and peer tables share the union");
   for (int i = tid; i < NWV * kRankRadix; i += NT) mt[i / kRankRadix][i % kRankRadix] = 0;
-  uint32_t key[ITEMS];
-  if (npass > 0) load_tile<uint32_t, ITEMS>(keys, n2, key);
+  // SAME sorts the T write keys (their address above tbits), otherwise the
+  // 2T merged keys (above tbits + 1)
+  constexpr int SI = SAME ? ITEMS / 2 : ITEMS;
+  const int ns = SAME ? (int)T : n2;
+  const int sh0 = SAME ? tbits : tb1;
+  uint32_t key[SI];
+  if (npass > 0) load_tile<uint32_t, SI>(keys, ns, key);
   for (int p = 0; p < npass; ++p) {
-    const int shift = tb1 + 8 * p;
-    uint32_t rank[ITEMS];
+    const int shift = sh0 + 8 * p;
+    uint32_t rank[SI];
     uint32_t own;
-    rank_tile<uint32_t, ITEMS, NT, true>(n2, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
+    rank_tile<uint32_t, SI, NT, true>(ns, shift, wcnt, dstart, scan_tmp, key, rank, &own, mt);
     __syncthreads();  // dstart of every digit; every thread's keys are in registers
 #pragma unroll
-    for (int it = 0; it < ITEMS; ++it) {
-      const int i = wv * kWave * ITEMS + it * kWave + lane;
-      if (i < n2) {
+    for (int it = 0; it < SI; ++it) {
+      const int i = wv * kWave * SI + it * kWave + lane;
+      if (i < ns) {
         const uint32_t d = (key[it] >> shift) & (kRankRadix - 1);
         keys[dstart[d] + wcnt[wv][d] + rank[it]] = key[it];
       }
     }
     __syncthreads();
-    if (p + 1 < npass) load_tile<uint32_t, ITEMS>(keys, n2, key);
+    if (p + 1 < npass) load_tile<uint32_t, SI>(keys, ns, key);
   }
   __syncthreads();
   // 2. one code word per item, over its key: bits 0..23 the time, bit 29 a
   // run start, bit 30 no store (a write), bit 31 no load (a read, or a write
   // no later read of its run needs).  Items [n2, n2r) pad the walkers'
   // ranges to whole batches as writes that are not loaded.
-  const bool table = A <= kMergedLr;
+  const bool table = !SAME && A <= kMergedLr;
   uint32_t* lr = (uint32_t*)(un + NWV * kRankRadix * sizeof(uint32_t));  // last read + 1
   if (table) {
     for (int i = tid; i < A; i += NT) lr[i] = 0u;
@@ -968,7 +998,33 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   }
   const int n2r = (n2 + WB - 1) & ~(WB - 1);  // <= kMergedItems
   const uint32_t tmask1 = (1u << tb1) - 1u;
-  {
+  if constexpr (SAME) {
+    // sorted record i: its read (a run start when the address changes; not
+    // loaded) and its write (loaded when the next record shares the address,
+    // whose read follows it)
+    const uint32_t tmask = (1u << tbits) - 1u;
+    uint32_t cr[SI], cwt[SI];
+#pragma unroll
+    for (int m = 0; m < SI; ++m) {
+      const int i = m * NT + tid;
+      cr[m] = cwt[m] = kCodeNoLoad | kCodeNoStore;
+      if (i < ns) {
+        const uint32_t k = keys[i];
+        const uint32_t a = k >> tbits;
+        const bool st = i == 0 || (keys[i - 1] >> tbits) != a;
+        const bool need = i + 1 < ns && (keys[i + 1] >> tbits) == a;
+        cr[m] = (st ? kCodeStart : 0u) | kCodeNoLoad | (k & tmask);
+        cwt[m] = kCodeNoStore | (need ? 0u : kCodeNoLoad) | (k & tmask);
+      }
+    }
+    __syncthreads();  // every key is read
+#pragma unroll
+    for (int m = 0; m < SI; ++m) {
+      const int i = m * NT + tid;
+      if (i < ns) *(u32x2*)&keys[2 * i] = u32x2{cr[m], cwt[m]};
+    }
+    if (tid < n2r - n2) keys[n2 + tid] = kCodeNoLoad | kCodeNoStore;
+  } else {
     uint32_t cw[ITEMS];
 #pragma unroll
     for (int m = 0; m < ITEMS; ++m) {
@@ -1304,7 +1360,7 @@ bool merged_applies(const Tape& tp, int64_t row_bytes, const void* payload, cons
 }
 
 // Ring size of the merged kernel's latest-k sources (0: none).
-int merged_ring(int64_t k) { return k < 1 ? 0 : (k == 1 ? 1 : (k <= 4 ? 4 : 8)); }
+int merged_ring(int64_t k) { return k < 1 ? 0 : (k <= 4 ? 4 : 8); }
 
 // The merged kernel also makes the latest-k lookup: k <= 8, the walkers'
 // tail rings fit their LDS, and the value rows and sources of a segment sit
@@ -1341,26 +1397,33 @@ hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* w
   static std::atomic<uint32_t> launches{0};
   const uint32_t tag = (launches.fetch_add(1, std::memory_order_relaxed) + 1u) & 0xffffu;
   uint32_t* gate = tp.status + kStatusGateWord;
-#define REM_MG(IT, KS)                                                                       \
-  segsum_merged_kernel<IT, KS, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(                 \
+  // reads at the write addresses and no mask: sort the write keys only
+  const bool same = !ra && !wmask;
+#define REM_MG(IT, KS, SM)                                                                     \
+  segsum_merged_kernel<IT, KS, SM, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(             \
       wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
       tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
       tag, gate_lo, gate_hi, target, ticks, k, (S*)vout, vmask, osrc, vtemp)
-#define REM_MG_KS(IT)                           \
+#define REM_MG_KS(IT, SM)                        \
   switch (vout ? merged_ring(k) : 0) {          \
-    case 0: REM_MG(IT, 0); break;               \
-    case 1: REM_MG(IT, 1); break;               \
-    case 4: REM_MG(IT, 4); break;               \
-    default: REM_MG(IT, 8); break;              \
+    case 0: REM_MG(IT, 0, SM); break;           \
+    case 4: REM_MG(IT, 4, SM); break;           \
+    default: REM_MG(IT, 8, SM); break;          \
   }
   if (vout && (!vmask || !merged_values_apply(tp, G * 16, k))) return hipErrorInvalidValue;
   // value rows through the caches while they fit the 256 MB last-level cache
   // twice over (measured faster up to 268 MB; streamed past it)
   const int vtemp = tp.n() * k * G * 16 <= ((int64_t)512 << 20) ? 1 : 0;
   if (2 * tp.T <= 4 * kMergedThreads) {
-    REM_MG_KS(4);
+    if (same) {
+      REM_MG_KS(4, true);
+    } else {
+      REM_MG_KS(4, false);
+    }
+  } else if (same) {
+    REM_MG_KS(16, true);
   } else {
-    REM_MG_KS(16);
+    REM_MG_KS(16, false);
   }
 #undef REM_MG_KS
 #undef REM_MG
