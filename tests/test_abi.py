@@ -173,6 +173,26 @@ def test_invalid_arguments_rejected_without_launch():
     assert rc == 1 and "null" in _err()
     rc = lib.ravel_em_cache_read(None, None, None, nat.INT64, nat.BFLOAT16, 2, 3, 0, 1, 4, None, None, None)
     assert rc == 1 and "cache shape" in _err()
+    # the joint latest-k + sum entry point checks the union of both operators' arguments
+    joint = lambda *a: lib.ravel_em_latest_k_sum_fwd(*a)
+    rc = joint(None, None, nat.INT64, None, None, nat.FLOAT32, 2, 3, 4, 5, 7, 0,
+               None, None, None, None, None, None, 0, None)
+    assert rc == 1 and "k must be positive" in _err()
+    rc = joint(None, None, 7, None, None, nat.FLOAT32, 2, 3, 4, 5, 7, 1,
+               None, None, None, None, None, None, 0, None)
+    assert rc == 1 and "address dtype" in _err()
+    rc = joint(None, None, nat.INT64, None, None, 99, 2, 3, 4, 5, 7, 1,
+               None, None, None, None, None, None, 0, None)
+    assert rc == 1 and "payload dtype" in _err()
+    rc = joint(fake, None, nat.INT64, None, fake, nat.FLOAT32, 2, 3, 4, 5, 7, 1,
+               fake, fake, None, None, fake, None, 0, None)
+    assert rc == 1 and "null" in _err()  # no sum output
+    rc = joint(None, None, nat.INT64, None, None, nat.FLOAT32, 2, 1 << 27, 1 << 4, 5, 7, 1,
+               None, None, None, None, None, None, 0, None)
+    assert rc == 1 and "one batch row" in _err()
+    rc = joint(None, None, nat.INT64, None, None, nat.FLOAT32, 1 << 20, 1 << 12, 1 << 4, 5, 7, 1,
+               None, None, fake, None, None, None, 0, None)
+    assert rc == 1 and "int32 sources" in _err()
 
 
 def test_workspace_too_small_is_reported_before_launch():
@@ -181,12 +201,24 @@ def test_workspace_too_small_is_reported_before_launch():
     rc = lib.ravel_em_latest_k_fwd(fake, None, nat.INT64, None, fake, nat.FLOAT32,
                                    2, 64, 3, 4, 11, 1, fake, fake, None, fake, 16, None)
     assert rc == 3 and "workspace" in _err()
+    # the joint call in each of its forms (short tape, long tape, the pair for k > 8)
+    for (T, k) in [(64, 2), (6000, 1), (64, 12)]:
+        need = lib.ravel_em_latest_k_sum_workspace(2, T, 3, 8, 11, k, 0, 0, 0, nat.BFLOAT16)
+        assert need > 16
+        rc = lib.ravel_em_latest_k_sum_fwd(fake, None, nat.INT64, None, fake, nat.BFLOAT16,
+                                           2, T, 3, 8, 11, k, fake, fake, None, fake, fake,
+                                           fake, 16, None)
+        assert rc == 3 and "workspace" in _err(), (T, k)
 
 
 def test_empty_tape_is_a_no_op():
     lib = nat.library()
     rc = lib.ravel_em_latest_k_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
                                    0, 3, 4, 5, 7, 1, None, None, None, None, 0, None)
+    assert rc == 0
+    rc = lib.ravel_em_latest_k_sum_fwd(None, None, nat.INT64, None, None, nat.FLOAT32,
+                                       0, 3, 4, 5, 7, 1, None, None, None, None, None, None, 0,
+                                       None)
     assert rc == 0
 
 

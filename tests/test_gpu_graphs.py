@@ -9,7 +9,8 @@ against the eager call.
 import pytest
 import torch
 
-from ravel_em import RavelLayerCache, causal_last_k_lookup, causal_sum_lookup
+from ravel_em import (RavelLayerCache, causal_last_k_and_sum_lookup, causal_last_k_lookup,
+                      causal_sum_lookup)
 
 pytestmark = pytest.mark.gpu
 
@@ -65,6 +66,21 @@ def test_sum_replays_match_eager(device, shape):
     _replay_matches(lambda: causal_sum_lookup(w, p, r, address_space=A), _noise(device))
 
 
+@pytest.mark.parametrize("shape", [(2, 300, 3, 40, 2, False), (2, 300, 3, 40, 4, True),
+                                   (1, 6000, 4, 5000, 1, False), (2, 700, 3, 23, 12, False)])
+def test_joint_replays_match_eager(device, shape):
+    """The joint call in its three forms (merged short tape, long-tape walker with
+    latest-1 values and the mask copy, and the two operators for k > 8)."""
+    B, T, C, A, k, sep = shape
+    print(f"[graph latest_k_sum] {shape}", flush=True)
+    g = torch.Generator().manual_seed(T + k)
+    w = torch.randint(0, A, (B, T, C), generator=g).to(device)
+    r = torch.randint(0, A, (B, T, C), generator=g).to(device) if sep else None
+    p = torch.randn(B, T, C, 16, generator=g).to(torch.bfloat16).to(device)
+    _replay_matches(lambda: causal_last_k_and_sum_lookup(w, p, r, address_space=A, k=k),
+                    _noise(device))
+
+
 def test_cache_step_replays_match_eager(device):
     """A captured decode step replays against a cache that the previous replay
     advanced: every replay equals the eager step on a copy of that cache."""
@@ -107,6 +123,29 @@ def test_torch_compile_traces_through_the_lookups(device):
     def f(w, p):
         vals, mask = causal_last_k_lookup(w, p, address_space=30, k=2)
         s, smask = causal_sum_lookup(w, p, address_space=30)
+        return vals.sum(dim=3) * mask.any(dim=3, keepdim=True) + s * smask.unsqueeze(-1)
+
+    compiled = torch.compile(f, backend="aot_eager", fullgraph=True)
+    pe = p.clone().requires_grad_(True)
+    pc = p.clone().requires_grad_(True)
+    want = f(w, pe)
+    got = compiled(w, pc)
+    assert torch.equal(got, want)
+    weights = torch.randn_like(want)
+    (want * weights).sum().backward()
+    (got * weights).sum().backward()
+    assert torch.allclose(pc.grad, pe.grad, rtol=1e-6, atol=1e-6)
+
+
+def test_torch_compile_traces_through_the_joint_lookup(device):
+    """fullgraph tracing goes through ravel_em::latest_k_sum (fake and autograd);
+    results and gradients equal the eager call's."""
+    g = torch.Generator().manual_seed(10)
+    w = torch.randint(0, 30, (2, 200, 3), generator=g).to(device)
+    p = torch.randn(2, 200, 3, 8, generator=g).to(device)
+
+    def f(w, p):
+        vals, mask, s, smask = causal_last_k_and_sum_lookup(w, p, address_space=30, k=2)
         return vals.sum(dim=3) * mask.any(dim=3, keepdim=True) + s * smask.unsqueeze(-1)
 
     compiled = torch.compile(f, backend="aot_eager", fullgraph=True)

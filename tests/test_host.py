@@ -6,7 +6,8 @@ import pytest
 import torch
 
 import ravel_em
-from ravel_em import RavelLayerCache, causal_last_k_lookup, causal_sum_lookup
+from ravel_em import (RavelLayerCache, causal_last_k_and_sum_lookup, causal_last_k_lookup,
+                      causal_sum_lookup)
 from ravel_em.ravel_memory import _composite_key_dtype
 
 
@@ -27,6 +28,10 @@ def test_public_names_match_reference_module():
     assert sig.parameters["k"].default == 1
     sig = inspect.signature(causal_sum_lookup)
     assert list(sig.parameters) == ["write_addresses", "payloads", "read_addresses", "address_space", "write_mask"]
+    # the joint call takes causal_last_k_lookup's arguments
+    sig = inspect.signature(causal_last_k_and_sum_lookup)
+    assert list(sig.parameters) == ["write_addresses", "payloads", "read_addresses", "address_space", "k", "write_mask"]
+    assert sig.parameters["address_space"].kind is inspect.Parameter.KEYWORD_ONLY
 
 
 def test_shape_errors_match_reference():
@@ -46,6 +51,12 @@ def test_shape_errors_match_reference():
         causal_last_k_lookup(a, p, address_space=8, write_mask=torch.ones(2, 4, dtype=torch.bool))
     with pytest.raises(ValueError, match="expected write_addresses"):
         causal_sum_lookup(a[0], p, address_space=8)
+    with pytest.raises(ValueError, match="same shape"):
+        causal_last_k_and_sum_lookup(a, p, torch.zeros(2, 5, 2, dtype=torch.long), address_space=8)
+    with pytest.raises(ValueError, match="k must be positive"):
+        causal_last_k_and_sum_lookup(a, p, address_space=8, k=0)
+    with pytest.raises(ValueError, match="write_mask"):
+        causal_last_k_and_sum_lookup(a, p, address_space=8, write_mask=torch.ones(2, 4, dtype=torch.bool))
 
 
 def test_cache_shape_errors_match_reference():
@@ -66,6 +77,8 @@ def test_cpu_tensors_raise_instead_of_falling_back():
         causal_last_k_lookup(a, p, address_space=8)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         causal_sum_lookup(a, p, address_space=8)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        causal_last_k_and_sum_lookup(a, p, address_space=8)
     cache = RavelLayerCache.empty(1, 2, 16, 3, device="cpu", dtype=torch.float32)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         cache.read(torch.tensor([[5, 7]]))
