@@ -90,6 +90,8 @@ CASES = [
     (2, 25, 2, 1, False, False, 2),     # one address: every run is the whole segment
     (2, 9, 2, 4, False, False, 8),
     (2, 300, 3, 2, False, True, 5),     # long runs over many walkers, per-slot stores
+    (40, 300, 8, 37, False, False, 4),  # more segments than CUs: 512-thread blocks
+    (40, 300, 8, 3, True, True, 8),
     (1, 3000, 2, 2, True, False, 8),    # runs far longer than two walker ranges
     (3, 4096, 2, 300, False, True, 4),  # the longest merged tape
     (2, 4096, 1, 1, False, False, 1),   # one run of 8192 items

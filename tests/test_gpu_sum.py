@@ -134,6 +134,8 @@ CASES = [
     (3, 40, 2, 5, True, False),
     (2, 33, 4, 7, True, True),
     (2, 25, 2, 1, False, False),
+    (40, 300, 8, 37, False, False),  # more segments than CUs: 512-thread blocks
+    (40, 300, 8, 3, True, True),
     (3, 5000, 2, 300, False, False),
     (1, 70000, 1, 2, False, False),  # runs spanning hundreds of chunks
     (1, 70000, 1, 3, True, True),
