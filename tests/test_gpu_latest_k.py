@@ -401,6 +401,26 @@ def test_multi_piece_buckets(device, case):
     check_against_oracle(w.to(device), p.to(device), A=A, k=1)
 
 
+@pytest.mark.parametrize("case", HOT, ids=[f"{n}-{T}-{A}" for n, T, A in HOT])
+def test_sort_order_hot_buckets(device, case):
+    """The full sort of the same tapes: with two address digits it scatters by
+    the high digit, then sorts each bucket by the low digit (a wave, a block,
+    or the parts of a large bucket, placed from the parts' histograms); the
+    keys and the order are the oracle's, and so is the segmented sum walked
+    over them."""
+    name, T, A = case
+    print(f"[hot sort] {name} T={T} A={A}", flush=True)
+    w = _hot_case(name, T, A)
+    keys, order = sort_order(w.to(device), address_space=A)
+    okeys, oorder = oracle.sort_order(w, address_space=A)
+    assert np.array_equal(keys.cpu().numpy().astype(np.int64), okeys)
+    assert np.array_equal(order.cpu().numpy(), oorder)
+    p = torch.randint(-3, 4, (*w.shape, 8)).float()  # small integers: exact sums
+    out, mask = causal_sum_lookup(w.to(device), p.to(device), address_space=A)
+    truth, tmask = oracle.seg_sum(w, p, address_space=A)
+    assert torch.equal(out.cpu().double(), truth) and torch.equal(mask.cpu(), tmask)
+
+
 def test_eager_fast_path_matches_the_registered_op(device):
     """The public calls without autograd run the ops' bodies directly; the
     registered ops (the autograd and torch.compile route) give the same bits."""
