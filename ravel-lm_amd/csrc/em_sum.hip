@@ -1123,19 +1123,27 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
         if (i0 + m < from || i0 + m >= to) cw[m] = kPad;
 #pragma unroll
       for (int m = 0; m < WB; ++m)
-        x[m] = __builtin_amdgcn_raw_buffer_load_b128(
-            prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad), 0, aux);
+        x[m] = SAME && !(m & 1) ? u32x4{0u, 0u, 0u, 0u}  // a read: never loaded
+                                : __builtin_amdgcn_raw_buffer_load_b128(
+                                      prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad),
+                                      0, aux);
     };
+    // SAME: batches start at even items, so item m of a batch is the read of
+    // its record when m is even and the write when m is odd (pads, outside
+    // [from, to) or past the tape, store nothing either way, and the ring a
+    // pad moves before a run start is reset there): each item does only its
+    // kind's part of the work below.
     auto process = [&](const uint32_t* cw, const u32x4* x) {
 #pragma unroll
       for (int m = 0; m < WB; ++m) {
         const uint32_t k = cw[m];
-        const bool st = k & kCodeStart;
+        const bool rd = SAME ? !(m & 1) : !(k & kCodeNoStore);  // (SAME: known per m)
+        const bool st = (!SAME || rd) && (k & kCodeStart);  // run starts are reads
 #pragma unroll
         for (int j = 0; j < CPU; ++j) acc[j] = st ? Acc(0) : acc[j];
         hasw = hasw && !st;
         rcnt = st ? 0 : rcnt;
-        if (STORE) {
+        if (STORE && (!SAME || rd)) {
           const uint32_t ns = k & kCodeNoStore;
           // with KS > 0 the sums share the write stream with k times their
           // bytes of value rows and skip the caches; alone they go through L2
@@ -1146,8 +1154,8 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
         }
         if constexpr (KS > 0) {
           const uint32_t ns = k & kCodeNoStore;  // a write: it stores nothing, it enters the ring
-          const bool wr = ns != 0;
-          if (STORE) {
+          const bool wr = SAME ? (m & 1) != 0 : ns != 0;
+          if (STORE && (!SAME || rd)) {
             const uint32_t vo = __umul24(k, vstride) | ns;
             const u32x4 z = {0u, 0u, 0u, 0u};
             // value rows of small tapes stay in the caches, larger ones stream
@@ -1163,6 +1171,8 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
             if (osrc)
               store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, ring, rcnt, kslots,
                                 rbase32, Ci);
+          }
+          if (STORE && (!SAME || wr)) {
 #pragma unroll
             for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
             vring[0] = wr ? x[m] : vring[0];
@@ -1172,8 +1182,10 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
           ring[0] = wr ? (k & kCodeTime) : ring[0];
           rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
         }
-        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
-        hasw = hasw || !(k & kCodeNoLoad);
+        if (!SAME || !rd) {
+          add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
+          hasw = hasw || !(k & kCodeNoLoad);
+        }
       }
     };
     for (int i0 = from & ~(WB - 1); i0 < to; i0 += WB) {
