@@ -863,6 +863,11 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   // walk batch: 16 items, 8 with fp64 sums (their conversions need the
   // registers that a wider batch would take) or rings of rows
   constexpr int WB = sizeof(Acc) == sizeof(float) && KS == 0 ? 16 : 8;
+  // items a walk takes per loop iteration: with the ring of SAME turning by
+  // one slot per write (WB / 2 writes a batch), whole turns of KS slots
+  constexpr int NB = SAME && KS > 0 ? (KS > WB / 2 ? KS / (WB / 2) : 1) : 1;
+  constexpr int WBI = NB * WB;
+  static_assert(!SAME || KS == 0 || (NB * (WB / 2)) % KS == 0, "whole turns of the ring");
   __shared__ __align__(16) uint32_t keys[kMergedItems];
   __shared__ __align__(16) unsigned char un[kMergedUnion];
   __shared__ uint32_t dstart[kRankRadix];
@@ -996,7 +1001,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
     __syncthreads();
   }
-  const int n2r = (n2 + WB - 1) & ~(WB - 1);  // <= kMergedItems
+  const int n2r = (n2 + WBI - 1) & ~(WBI - 1);  // <= kMergedItems
   const uint32_t tmask1 = (1u << tb1) - 1u;
   if constexpr (SAME) {
     // sorted record i: its read (a run start when the address changes; not
@@ -1052,7 +1057,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   // 3. the walk: walker w owns items [rs, re), whole batches
   const int NW = NT / G;
   const int w = tid / G, v = tid - (tid / G) * G;
-  const int len = (((n2r + NW - 1) / NW) + WB - 1) & ~(WB - 1);
+  const int len = (((n2r + NW - 1) / NW) + WBI - 1) & ~(WBI - 1);
   const int rs = w * len < n2r ? w * len : n2r;
   const int re = (rs + len) < n2r ? (rs + len) : n2r;
   // The segment's rows through buffer descriptors: row t's unit v is at byte
@@ -1133,7 +1138,14 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     // [from, to) or past the tape, store nothing either way, and the ring a
     // pad moves before a run start is reset there): each item does only its
     // kind's part of the work below.
-    auto process = [&](const uint32_t* cw, const u32x4* x) {
+    // SAME with KS > 0: the ring turns instead of shifting.  Before item m of
+    // batch BI of an iteration, wbf writes of the iteration have entered it,
+    // and logical slot j (0 the newest) sits at physical index (j + R) % KR;
+    // a write fills the oldest slot's index, R - 1.  Index arithmetic on
+    // constants only (the loops unroll), and a walk ends every iteration (and
+    // so itself) with R = 0: the logical order the long-run carry reads.
+    auto process = [&](const uint32_t* cw, const u32x4* x, auto bi_tag) {
+      constexpr int BI = decltype(bi_tag)::value;
 #pragma unroll
       for (int m = 0; m < WB; ++m) {
         const uint32_t k = cw[m];
@@ -1155,32 +1167,47 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
         if constexpr (KS > 0) {
           const uint32_t ns = k & kCodeNoStore;  // a write: it stores nothing, it enters the ring
           const bool wr = SAME ? (m & 1) != 0 : ns != 0;
+          const int wbf = BI * (WB / 2) + m / 2;
+          const int R = SAME ? (KR - wbf % KR) % KR : 0;
           if (STORE && (!SAME || rd)) {
             const uint32_t vo = __umul24(k, vstride) | ns;
             const u32x4 z = {0u, 0u, 0u, 0u};
             // value rows of small tapes stay in the caches, larger ones stream
 #pragma unroll
             for (int j = 0; j < KR; ++j) {
-              const u32x4 val = j < rcnt ? vring[j] : z;
+              const u32x4 val = j < rcnt ? vring[(j + R) % KR] : z;
               const uint32_t off = (vo + (uint32_t)j * rowb + v16) | (j < kslots ? 0u : 0x80000000u);
               if (vtemp)
                 __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, 0);
               else
                 __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, kBufNontemporal);
             }
-            if (osrc)
-              store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, ring, rcnt, kslots,
+            if (osrc) {
+              uint32_t rl[KR];  // the times in logical order
+#pragma unroll
+              for (int j = 0; j < KR; ++j) rl[j] = ring[(j + R) % KR];
+              store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, rl, rcnt, kslots,
                                 rbase32, Ci);
+            }
           }
-          if (STORE && (!SAME || wr)) {
+          if constexpr (SAME) {
+            if (wr) {  // known per m
+              const int p = (R + KR - 1) % KR;
+              if (STORE) vring[p] = x[m];
+              ring[p] = k & kCodeTime;
+              rcnt = rcnt < KS ? rcnt + 1 : KS;
+            }
+          } else {
+            if (STORE) {
 #pragma unroll
-            for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
-            vring[0] = wr ? x[m] : vring[0];
+              for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
+              vring[0] = wr ? x[m] : vring[0];
+            }
+#pragma unroll
+            for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
+            ring[0] = wr ? (k & kCodeTime) : ring[0];
+            rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
           }
-#pragma unroll
-          for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
-          ring[0] = wr ? (k & kCodeTime) : ring[0];
-          rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
         }
         if (!SAME || !rd) {
           add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
@@ -1188,11 +1215,15 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
         }
       }
     };
-    for (int i0 = from & ~(WB - 1); i0 < to; i0 += WB) {
+    for (int i0 = from & ~(WBI - 1); i0 < to; i0 += WBI) {
       uint32_t cw[WB];
       u32x4 x[WB];
       fetch(i0, cw, x);
-      process(cw, x);
+      process(cw, x, std::integral_constant<int, 0>{});
+      if constexpr (NB == 2) {  // (n2r and the walkers' ranges are whole iterations)
+        fetch(i0 + WB, cw, x);
+        process(cw, x, std::integral_constant<int, 1>{});
+      }
     }
   };
 
