@@ -91,6 +91,9 @@ CASES = [
     (2, 9, 2, 4, False, False, 8),
     (2, 300, 3, 2, False, True, 5),     # long runs over many walkers, per-slot stores
     (40, 300, 8, 37, False, False, 4),  # more segments than CUs: 512-thread blocks
+    (2, 1000, 3, 2, False, False, 8),   # reads at the writes, k = 8: long runs, carried ring
+    (1, 4096, 2, 3, False, False, 6),   # the same at T = 4096, k = 6 of a ring of 8
+    (3, 700, 2, 5, False, False, 3),    # k = 3 of a ring of 4, long runs
     (40, 300, 8, 3, True, True, 8),
     (1, 3000, 2, 2, True, False, 8),    # runs far longer than two walker ranges
     (3, 4096, 2, 300, False, True, 4),  # the longest merged tape
