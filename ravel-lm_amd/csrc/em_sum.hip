@@ -845,7 +845,10 @@ __device__ __forceinline__ void store_sources(__amdgpu_buffer_rsrc_t rs, uint32_
   }
 }
 
-template <int ITEMS, int KS, bool SAME, typename XIn, typename Acc, typename LoadF, typename StoreF>
+// VT (KS > 0): value rows through the caches, else streamed (a constant of the
+// instantiation: a branch per store on the launch's choice cost 2 % at cfg3).
+template <int ITEMS, int KS, bool SAME, bool VT, typename XIn, typename Acc, typename LoadF,
+          typename StoreF>
 __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void segsum_merged_kernel(
     const void* __restrict__ waddr, int wkind, const void* __restrict__ raddr, int rkind,
     const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int trunc32, int tbits,
@@ -853,7 +856,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     XIn* __restrict__ out, uint8_t* __restrict__ omask, uint32_t* __restrict__ status,
     uint32_t* __restrict__ gate, uint32_t tag, uint32_t gate_lo, uint32_t gate_hi,
     uint32_t gate_target, uint32_t gate_ticks, int kslots, XIn* __restrict__ vout,
-    uint8_t* __restrict__ vmask, int32_t* __restrict__ osrc, int vtemp) {
+    uint8_t* __restrict__ vmask, int32_t* __restrict__ osrc) {
   constexpr int NT = kMergedThreads;
   constexpr int NWV = NT / kWave;
   constexpr int CPU = 16 / (int)sizeof(XIn);  // columns per lane
@@ -1177,10 +1180,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
             for (int j = 0; j < KR; ++j) {
               const u32x4 val = j < rcnt ? vring[(j + R) % KR] : z;
               const uint32_t off = (vo + (uint32_t)j * rowb + v16) | (j < kslots ? 0u : 0x80000000u);
-              if (vtemp)
-                __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, 0);
-              else
-                __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, kBufNontemporal);
+              __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, VT ? 0 : kBufNontemporal);
             }
             if (osrc) {
               uint32_t rl[KR];  // the times in logical order
@@ -1442,16 +1442,20 @@ hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* w
   uint32_t* gate = tp.status + kStatusGateWord;
   // reads at the write addresses and no mask: sort the write keys only
   const bool same = !ra && !wmask;
-#define REM_MG(IT, KS, SM)                                                                     \
-  segsum_merged_kernel<IT, KS, SM, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(             \
+#define REM_MG(IT, KS, SM, VT)                                                                 \
+  segsum_merged_kernel<IT, KS, SM, VT, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(         \
       wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
       tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
-      tag, gate_lo, gate_hi, target, ticks, k, (S*)vout, vmask, osrc, vtemp)
-#define REM_MG_KS(IT, SM)                        \
-  switch (vout ? merged_ring(k) : 0) {          \
-    case 0: REM_MG(IT, 0, SM); break;           \
-    case 4: REM_MG(IT, 4, SM); break;           \
-    default: REM_MG(IT, 8, SM); break;          \
+      tag, gate_lo, gate_hi, target, ticks, k, (S*)vout, vmask, osrc)
+#define REM_MG_KS(IT, SM)                                                 \
+  switch (vout ? merged_ring(k) : 0) {                                   \
+    case 0: REM_MG(IT, 0, SM, false); break;                             \
+    case 4:                                                              \
+      if (vtemp) REM_MG(IT, 4, SM, true); else REM_MG(IT, 4, SM, false); \
+      break;                                                             \
+    default:                                                             \
+      if (vtemp) REM_MG(IT, 8, SM, true); else REM_MG(IT, 8, SM, false); \
+      break;                                                             \
   }
   if (vout && (!vmask || !merged_values_apply(tp, G * 16, k))) return hipErrorInvalidValue;
   // value rows through the caches while they fit the 256 MB last-level cache
