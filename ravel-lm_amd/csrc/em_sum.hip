@@ -1115,114 +1115,115 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   // loaded write adds its row, a read (STORE) stores the sum and the flag.
   // The final walk streams the rows it reads past the caches (its stores go
   // through L2, which measured faster than streaming them).
-  auto walk = [&](int from, int to, auto store_tag) {
-    constexpr bool STORE = decltype(store_tag)::value;
-    constexpr int aux = STORE ? kBufNontemporal : 0;
+  // the code words of batch i0 and their rows (every load in flight); items
+  // outside [from, to) are pads
+  auto fetch = [&](int i0, int from, int to, auto store_tag, uint32_t* cw, u32x4* x) {
+    constexpr int aux = decltype(store_tag)::value ? kBufNontemporal : 0;
     constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
-    // the code words of batch i0 and their rows (every load in flight)
-    auto fetch = [&](int i0, uint32_t* cw, u32x4* x) {
 #pragma unroll
-      for (int q = 0; q < WB / 4; ++q) {
-        const u32x4 c4 = *(const u32x4*)&keys[i0 + 4 * q];
-        cw[4 * q] = c4.x, cw[4 * q + 1] = c4.y, cw[4 * q + 2] = c4.z, cw[4 * q + 3] = c4.w;
+    for (int q = 0; q < WB / 4; ++q) {
+      const u32x4 c4 = *(const u32x4*)&keys[i0 + 4 * q];
+      cw[4 * q] = c4.x, cw[4 * q + 1] = c4.y, cw[4 * q + 2] = c4.z, cw[4 * q + 3] = c4.w;
+    }
+#pragma unroll
+    for (int m = 0; m < WB; ++m)
+      if (i0 + m < from || i0 + m >= to) cw[m] = kPad;
+#pragma unroll
+    for (int m = 0; m < WB; ++m)
+      x[m] = SAME && !(m & 1) ? u32x4{0u, 0u, 0u, 0u}  // a read: never loaded
+                              : __builtin_amdgcn_raw_buffer_load_b128(
+                                    prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad),
+                                    0, aux);
+  };
+  // SAME: batches start at even items, so item m of a batch is the read of
+  // its record when m is even and the write when m is odd (pads, outside
+  // [from, to) or past the tape, store nothing either way, and the ring a
+  // pad moves before a run start is reset there): each item does only its
+  // kind's part of the work below.
+  // SAME with KS > 0: the ring turns instead of shifting.  Before item m of
+  // batch BI of an iteration, wbf writes of the iteration have entered it,
+  // and logical slot j (0 the newest) sits at physical index (j + R) % KR;
+  // a write fills the oldest slot's index, R - 1.  Index arithmetic on
+  // constants only (the loops unroll), and a walk ends every iteration (and
+  // so itself) with R = 0: the logical order the long-run carry reads.
+  auto process = [&](const uint32_t* cw, const u32x4* x, auto bi_tag, auto store_tag) {
+    constexpr int BI = decltype(bi_tag)::value;
+    constexpr bool STORE = decltype(store_tag)::value;
+#pragma unroll
+    for (int m = 0; m < WB; ++m) {
+      const uint32_t k = cw[m];
+      const bool rd = SAME ? !(m & 1) : !(k & kCodeNoStore);  // (SAME: known per m)
+      const bool st = (!SAME || rd) && (k & kCodeStart);  // run starts are reads
+#pragma unroll
+      for (int j = 0; j < CPU; ++j) acc[j] = st ? Acc(0) : acc[j];
+      hasw = hasw && !st;
+      rcnt = st ? 0 : rcnt;
+      if (STORE && (!SAME || rd)) {
+        const uint32_t ns = k & kCodeNoStore;
+        // with KS > 0 the sums share the write stream with k times their
+        // bytes of value rows and skip the caches; alone they go through L2
+        __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XIn, StoreF, Acc, CPU>(acc), ors,
+                                               (__umul24(k, tstride) + v16) | ns, 0,
+                                               KS > 0 ? kBufNontemporal : 0);
+        hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = KS > 0 ? (uint8_t)rcnt : (hasw ? 1 : 0);
       }
-#pragma unroll
-      for (int m = 0; m < WB; ++m)
-        if (i0 + m < from || i0 + m >= to) cw[m] = kPad;
-#pragma unroll
-      for (int m = 0; m < WB; ++m)
-        x[m] = SAME && !(m & 1) ? u32x4{0u, 0u, 0u, 0u}  // a read: never loaded
-                                : __builtin_amdgcn_raw_buffer_load_b128(
-                                      prs, (__umul24(cw[m], tstride) + v16) | (cw[m] & kCodeNoLoad),
-                                      0, aux);
-    };
-    // SAME: batches start at even items, so item m of a batch is the read of
-    // its record when m is even and the write when m is odd (pads, outside
-    // [from, to) or past the tape, store nothing either way, and the ring a
-    // pad moves before a run start is reset there): each item does only its
-    // kind's part of the work below.
-    // SAME with KS > 0: the ring turns instead of shifting.  Before item m of
-    // batch BI of an iteration, wbf writes of the iteration have entered it,
-    // and logical slot j (0 the newest) sits at physical index (j + R) % KR;
-    // a write fills the oldest slot's index, R - 1.  Index arithmetic on
-    // constants only (the loops unroll), and a walk ends every iteration (and
-    // so itself) with R = 0: the logical order the long-run carry reads.
-    auto process = [&](const uint32_t* cw, const u32x4* x, auto bi_tag) {
-      constexpr int BI = decltype(bi_tag)::value;
-#pragma unroll
-      for (int m = 0; m < WB; ++m) {
-        const uint32_t k = cw[m];
-        const bool rd = SAME ? !(m & 1) : !(k & kCodeNoStore);  // (SAME: known per m)
-        const bool st = (!SAME || rd) && (k & kCodeStart);  // run starts are reads
-#pragma unroll
-        for (int j = 0; j < CPU; ++j) acc[j] = st ? Acc(0) : acc[j];
-        hasw = hasw && !st;
-        rcnt = st ? 0 : rcnt;
+      if constexpr (KS > 0) {
+        const uint32_t ns = k & kCodeNoStore;  // a write: it stores nothing, it enters the ring
+        const bool wr = SAME ? (m & 1) != 0 : ns != 0;
+        const int wbf = BI * (WB / 2) + m / 2;
+        const int R = SAME ? (KR - wbf % KR) % KR : 0;
         if (STORE && (!SAME || rd)) {
-          const uint32_t ns = k & kCodeNoStore;
-          // with KS > 0 the sums share the write stream with k times their
-          // bytes of value rows and skip the caches; alone they go through L2
-          __builtin_amdgcn_raw_buffer_store_b128(pack_unit<XIn, StoreF, Acc, CPU>(acc), ors,
-                                                 (__umul24(k, tstride) + v16) | ns, 0,
-                                                 KS > 0 ? kBufNontemporal : 0);
-          hm[ns ? kMergedItems / 2 : (k & kCodeTime)] = KS > 0 ? (uint8_t)rcnt : (hasw ? 1 : 0);
-        }
-        if constexpr (KS > 0) {
-          const uint32_t ns = k & kCodeNoStore;  // a write: it stores nothing, it enters the ring
-          const bool wr = SAME ? (m & 1) != 0 : ns != 0;
-          const int wbf = BI * (WB / 2) + m / 2;
-          const int R = SAME ? (KR - wbf % KR) % KR : 0;
-          if (STORE && (!SAME || rd)) {
-            const uint32_t vo = __umul24(k, vstride) | ns;
-            const u32x4 z = {0u, 0u, 0u, 0u};
-            // value rows of small tapes stay in the caches, larger ones stream
+          const uint32_t vo = __umul24(k, vstride) | ns;
+          const u32x4 z = {0u, 0u, 0u, 0u};
+          // value rows of small tapes stay in the caches, larger ones stream
 #pragma unroll
-            for (int j = 0; j < KR; ++j) {
-              const u32x4 val = j < rcnt ? vring[(j + R) % KR] : z;
-              const uint32_t off = (vo + (uint32_t)j * rowb + v16) | (j < kslots ? 0u : 0x80000000u);
-              __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, VT ? 0 : kBufNontemporal);
-            }
-            if (osrc) {
-              uint32_t rl[KR];  // the times in logical order
-#pragma unroll
-              for (int j = 0; j < KR; ++j) rl[j] = ring[(j + R) % KR];
-              store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, rl, rcnt, kslots,
-                                rbase32, Ci);
-            }
+          for (int j = 0; j < KR; ++j) {
+            const u32x4 val = j < rcnt ? vring[(j + R) % KR] : z;
+            const uint32_t off = (vo + (uint32_t)j * rowb + v16) | (j < kslots ? 0u : 0x80000000u);
+            __builtin_amdgcn_raw_buffer_store_b128(val, vrs, off, 0, VT ? 0 : kBufNontemporal);
           }
-          if constexpr (SAME) {
-            if (wr) {  // known per m
-              const int p = (R + KR - 1) % KR;
-              if (STORE) vring[p] = x[m];
-              ring[p] = k & kCodeTime;
-              rcnt = rcnt < KS ? rcnt + 1 : KS;
-            }
-          } else {
-            if (STORE) {
+          if (osrc) {
+            uint32_t rl[KR];  // the times in logical order
 #pragma unroll
-              for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
-              vring[0] = wr ? x[m] : vring[0];
-            }
-#pragma unroll
-            for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
-            ring[0] = wr ? (k & kCodeTime) : ring[0];
-            rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
+            for (int j = 0; j < KR; ++j) rl[j] = ring[(j + R) % KR];
+            store_sources<KS>(srs, (__umul24(k, sstride) | ns) | slane, rl, rcnt, kslots,
+                              rbase32, Ci);
           }
         }
-        if (!SAME || !rd) {
-          add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
-          hasw = hasw || !(k & kCodeNoLoad);
+        if constexpr (SAME) {
+          if (wr) {  // known per m
+            const int p = (R + KR - 1) % KR;
+            if (STORE) vring[p] = x[m];
+            ring[p] = k & kCodeTime;
+            rcnt = rcnt < KS ? rcnt + 1 : KS;
+          }
+        } else {
+          if (STORE) {
+#pragma unroll
+            for (int j = KR - 1; j > 0; --j) vring[j] = wr ? vring[j - 1] : vring[j];
+            vring[0] = wr ? x[m] : vring[0];
+          }
+#pragma unroll
+          for (int j = KR - 1; j > 0; --j) ring[j] = wr ? ring[j - 1] : ring[j];
+          ring[0] = wr ? (k & kCodeTime) : ring[0];
+          rcnt = wr ? (rcnt < KS ? rcnt + 1 : KS) : rcnt;
         }
       }
-    };
+      if (!SAME || !rd) {
+        add_unit<XIn, LoadF, Acc, CPU>(acc, x[m]);  // zeros where not loaded
+        hasw = hasw || !(k & kCodeNoLoad);
+      }
+    }
+  };
+  auto walk = [&](int from, int to, auto store_tag) {
     for (int i0 = from & ~(WBI - 1); i0 < to; i0 += WBI) {
       uint32_t cw[WB];
       u32x4 x[WB];
-      fetch(i0, cw, x);
-      process(cw, x, std::integral_constant<int, 0>{});
+      fetch(i0, from, to, store_tag, cw, x);
+      process(cw, x, std::integral_constant<int, 0>{}, store_tag);
       if constexpr (NB == 2) {  // (n2r and the walkers' ranges are whole iterations)
-        fetch(i0 + WB, cw, x);
-        process(cw, x, std::integral_constant<int, 1>{});
+        fetch(i0 + WB, from, to, store_tag, cw, x);
+        process(cw, x, std::integral_constant<int, 1>{}, store_tag);
       }
     }
   };
@@ -1271,10 +1272,38 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int j = 0; j < CPU; ++j) acc[j] = Acc(0);
   rcnt = 0;
-  walk(last >= 0 ? last : rs, re, std::false_type{});
+  // One iteration per walker (sums of short tapes of the reads-at-writes
+  // form): its rows are fetched once, for this tail pass and the final walk.
+  // A pass over the whole iteration ends with the tail's sums and flag, since
+  // a run start resets them.  (With rings the registers would not hold it.)
+  const bool one = SAME && KS == 0 && len == WBI;  // block-uniform
+  uint32_t cw1[WBI];
+  u32x4 x1[WBI];
+  if (one) {
+    if (rs < re) {
+      fetch(rs, rs, re, std::true_type{}, cw1, x1);
+      if constexpr (NB == 2) fetch(rs + WB, rs, re, std::true_type{}, cw1 + WB, x1 + WB);
+      process(cw1, x1, std::integral_constant<int, 0>{}, std::false_type{});
+      if constexpr (NB == 2)
+        process(cw1 + WB, x1 + WB, std::integral_constant<int, 1>{}, std::false_type{});
+    }
+  } else {
+    walk(last >= 0 ? last : rs, re, std::false_type{});
+  }
   const bool hwt = hasw;
   const int ncol = G * CPU;  // == D
-  Acc* tl = (Acc*)un;        // [walker][column]; the counters and table are dead
+  // The fold's thread (col, g) takes walkers [g*chunk, (g+1)*chunk) of column
+  // col (chunk <= 8).  Walker k's column sums sit at tl[k ncol + (k / chunk)
+  // pad + col]: the pad of 64 / NG accumulators after each group's walkers
+  // puts the 64 lanes of a wave (64 / NG columns of NG groups) on distinct
+  // LDS banks, where the groups of a column would otherwise share one.
+  const int NG = (NT / ncol) < 64 ? (NT / ncol) : 64;  // >= 1 (ncol <= 512)
+  const int chunk = NW / NG;
+  const int pad = kWave / NG;
+  static_assert(NT * CPU * sizeof(Acc) + kWave * sizeof(Acc) <= kMergedStartOff,
+                "walker tails and their pads stay below the first run starts");
+  Acc* tl = (Acc*)un;  // the counters and table are dead
+  const int tlw = w * ncol + (w / chunk) * pad + v * CPU;  // this lane's columns
   // KS > 0: each walker's tail ring ([walker][KS] times, then [walker] counts)
   uint32_t* rt = (uint32_t*)(un + kMergedRingOff);
   int* rc = (int*)(rt + NW * KR);
@@ -1287,7 +1316,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
   }
 #pragma unroll
-  for (int j = 0; j < CPU; ++j) tl[w * ncol + v * CPU + j] = acc[j];
+  for (int j = 0; j < CPU; ++j) tl[tlw + j] = acc[j];
   if (v == 0) {
     hs[w] = last >= 0 ? 1 : 0;
     hw[w] = hwt ? 1 : 0;
@@ -1295,23 +1324,30 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   __syncthreads();
   // fold: the carry into each walker, a segmented scan over the walkers (a
   // run start resets) of the column sums and of the has-a-write flags.
-  // Thread (col, g) folds walkers [g*chunk, (g+1)*chunk) of its column; the
-  // NG groups of a column are consecutive lanes of one wave (NG a power of two
-  // up to 64), which scan their aggregates with shuffles; then each thread
-  // rewrites its chunk with the carries.
+  // Thread (col, g) folds walkers [g*chunk, (g+1)*chunk) of its column (all
+  // of its loads at once); the NG groups of a column are consecutive lanes of
+  // one wave (NG a power of two up to 64), which scan their aggregates with
+  // shuffles; then each thread rewrites its chunk with the carries.
   {
-    const int NG = (NT / ncol) < 64 ? (NT / ncol) : 64;  // >= 1 (ncol <= 512)
-    const int chunk = NW / NG;
+    constexpr int CH = 8;  // chunk = CPU, or 8 / G when NG is capped at 64
     const int g = tid % NG, col = tid / NG;
+    const int base = g * chunk * ncol + g * pad + col;
+    Acc tv[CH];
+    bool sv[CH], wv8[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool in = i < chunk && col < ncol;
+      tv[i] = in ? tl[base + i * ncol] : Acc(0);
+      sv[i] = in && hs[g * chunk + i] != 0;
+      wv8[i] = in && hw[g * chunk + i] != 0;
+    }
     Acc x = Acc(0);
     bool f = false, h = false;
-    if (col < ncol) {
-      for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
-        const Acc t = tl[k * ncol + col];
-        x = hs[k] ? t : x + t;
-        h = hs[k] ? (hw[k] != 0) : (h || hw[k] != 0);
-        f = f || hs[k];
-      }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      x = sv[i] ? tv[i] : x + tv[i];
+      h = sv[i] ? wv8[i] : (h || wv8[i]);
+      f = f || sv[i];
     }
     // inclusive segmented scan over the column's groups, then shift by one
     for (int o = 1; o < NG; o <<= 1) {
@@ -1329,19 +1365,19 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
       cin = Acc(0);
       hin = false;
     }
-    if (col < ncol) {
-      for (int k = g * chunk; k < (g + 1) * chunk; ++k) {
-        const Acc t = tl[k * ncol + col];
-        tl[k * ncol + col] = cin;
-        cin = hs[k] ? t : cin + t;
-        if (col == 0) hwin[k] = hin ? 1 : 0;
-        hin = hs[k] ? (hw[k] != 0) : (hin || hw[k] != 0);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      if (i < chunk && col < ncol) {
+        tl[base + i * ncol] = cin;
+        if (col == 0) hwin[g * chunk + i] = hin ? 1 : 0;
       }
+      cin = sv[i] ? tv[i] : cin + tv[i];
+      hin = sv[i] ? wv8[i] : (hin || wv8[i]);
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < CPU; ++j) acc[j] = tl[w * ncol + v * CPU + j];
+  for (int j = 0; j < CPU; ++j) acc[j] = tl[tlw + j];
   hasw = hwin[w] != 0;
   if constexpr (KS > 0) {
     // the ring carried into the range: the newest writes of the earlier
@@ -1363,7 +1399,15 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
       vring[j] = __builtin_amdgcn_raw_buffer_load_b128(
           prs, (__umul24(ring[j], tstride) + v16) | (j < rcnt ? 0u : kCodeNoLoad), 0, 0);
   }
-  walk(rs, re, std::true_type{});
+  if (one) {
+    if (rs < re) {
+      process(cw1, x1, std::integral_constant<int, 0>{}, std::true_type{});
+      if constexpr (NB == 2)
+        process(cw1 + WB, x1 + WB, std::integral_constant<int, 1>{}, std::true_type{});
+    }
+  } else {
+    walk(rs, re, std::true_type{});
+  }
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t mrs =
