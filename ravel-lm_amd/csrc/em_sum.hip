@@ -1217,14 +1217,14 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   };
   auto walk = [&](int from, int to, auto store_tag) {
     for (int i0 = from & ~(WBI - 1); i0 < to; i0 += WBI) {
-      uint32_t cw[WB];
-      u32x4 x[WB];
+      // both batches' rows in flight before either is processed
+      uint32_t cw[WBI];
+      u32x4 x[WBI];
       fetch(i0, from, to, store_tag, cw, x);
+      if constexpr (NB == 2) fetch(i0 + WB, from, to, store_tag, cw + WB, x + WB);
       process(cw, x, std::integral_constant<int, 0>{}, store_tag);
-      if constexpr (NB == 2) {  // (n2r and the walkers' ranges are whole iterations)
-        fetch(i0 + WB, from, to, store_tag, cw, x);
-        process(cw, x, std::integral_constant<int, 1>{}, store_tag);
-      }
+      if constexpr (NB == 2)  // (n2r and the walkers' ranges are whole iterations)
+        process(cw + WB, x + WB, std::integral_constant<int, 1>{}, store_tag);
     }
   };
 
