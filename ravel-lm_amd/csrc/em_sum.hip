@@ -1113,12 +1113,14 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   // Items [from, to), in whole batches from the one holding `from` (items
   // outside are pads): a run start resets the sum and the has-a-write flag, a
   // loaded write adds its row, a read (STORE) stores the sum and the flag.
-  // The final walk streams the rows it reads past the caches (its stores go
-  // through L2, which measured faster than streaming them).
+  // The final walk of a sum streams the rows it reads past the caches (its
+  // stores go through L2, which measured faster than streaming them); with
+  // value rows (KS > 0) the rows stay cached, which measured faster when the
+  // payload has just been written (as by the layer op before the call).
   // the code words of batch i0 and their rows (every load in flight); items
   // outside [from, to) are pads
   auto fetch = [&](int i0, int from, int to, auto store_tag, uint32_t* cw, u32x4* x) {
-    constexpr int aux = decltype(store_tag)::value ? kBufNontemporal : 0;
+    constexpr int aux = decltype(store_tag)::value && KS == 0 ? kBufNontemporal : 0;
     constexpr uint32_t kPad = kCodeNoLoad | kCodeNoStore;
 #pragma unroll
     for (int q = 0; q < WB / 4; ++q) {

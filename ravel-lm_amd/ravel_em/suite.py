@@ -52,6 +52,34 @@ def time_calls(fn: Callable[[], object], warmup: int = 5, iters: int = 50) -> Li
     return [e0.elapsed_time(e1) * 1e3 for e0, e1 in events]
 
 
+def time_calls_fresh(fn: Callable[[], object], payload: torch.Tensor, warmup: int = 3,
+                     iters: int = 20) -> List[float]:
+    """Device microseconds of each of `iters` calls of fn, each made after a 1 GiB fill (more
+    than the last-level cache) and a rewrite of `payload`, as when the layer op before the
+    call has just written it.  Both are enqueued ahead of the call with no host wait, so the
+    events time the call's own kernels."""
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=payload.device)
+    src = payload.clone()
+
+    def prep(i: int) -> None:
+        flush.fill_(float(i))
+        payload.copy_(src)
+
+    for i in range(warmup):
+        prep(i)
+        fn()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for i, (e0, e1) in enumerate(events):
+        prep(i)
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    del flush, src
+    return [e0.elapsed_time(e1) * 1e3 for e0, e1 in events]
+
+
 def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) -> dict:
     gbps = nbytes / (us * 1e-6) / 1e9
     out = {
@@ -65,37 +93,42 @@ def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) ->
 
 def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None,
                ops=("latest_k", "seg_sum", "latest_k_sum")) -> List[dict]:
+    """Each line's us_per_call repeats the call back to back (the inputs it read in its previous
+    call may still be in the caches); us_fresh times it after a cache flush and a rewrite of
+    the payload (time_calls_fresh)."""
     B, T, C, D = w.shape
     lines = []
+
+    def timed(fn):
+        warm = statistics.median(time_calls(fn, iters=iters))
+        return warm, round(statistics.median(time_calls_fresh(fn, w.payload)), 2)
+
     if "latest_k_sum" in ops:
-        us = statistics.median(time_calls(
-            lambda: causal_last_k_and_sum_lookup(w.write, w.payload, w.read,
-                                                 address_space=w.address_space, k=w.k),
-            iters=iters))
+        us, fresh = timed(lambda: causal_last_k_and_sum_lookup(w.write, w.payload, w.read,
+                                                               address_space=w.address_space, k=w.k))
         lines.append(_line(w.name, "latest_k_sum", us, workloads.algorithmic_bytes_latest_k_sum(w),
                            B * T, shape=[B, T, C, D], k=w.k, A=w.address_space,
                            dtype=str(w.payload.dtype).split(".")[-1],
-                           read="separate" if w.read is not None else "same"))
+                           read="separate" if w.read is not None else "same", us_fresh=fresh))
     if "latest_k" in ops:
-        us = statistics.median(time_calls(
-            lambda: causal_last_k_lookup(w.write, w.payload, w.read, address_space=w.address_space, k=w.k),
-            iters=iters))
+        us, fresh = timed(lambda: causal_last_k_lookup(w.write, w.payload, w.read,
+                                                       address_space=w.address_space, k=w.k))
         lines.append(_line(w.name, "latest_k", us, workloads.algorithmic_bytes_latest_k(w), B * T,
                            shape=[B, T, C, D], k=w.k, A=w.address_space,
                            dtype=str(w.payload.dtype).split(".")[-1],
-                           read="separate" if w.read is not None else "same"))
+                           read="separate" if w.read is not None else "same", us_fresh=fresh))
     if "seg_sum" not in ops:
         if cpu is not None:
             for line in lines:
                 line["cpu_baseline"] = cpu(w, line["op"])
         return lines
-    us = statistics.median(time_calls(
-        lambda: causal_sum_lookup(w.write, w.payload, w.read, address_space=w.address_space), iters=iters))
+    us, fresh = timed(lambda: causal_sum_lookup(w.write, w.payload, w.read, address_space=w.address_space))
     N = B * T * C
     esz = w.payload.element_size()
     addr = N * w.write.element_size() * (1 if w.read is None else 2)
     sum_bytes = addr + N * D * esz + N * D * esz + N
-    lines.append(_line(w.name, "seg_sum", us, sum_bytes, B * T, shape=[B, T, C, D], A=w.address_space))
+    lines.append(_line(w.name, "seg_sum", us, sum_bytes, B * T, shape=[B, T, C, D], A=w.address_space,
+                       us_fresh=fresh))
     if cpu is not None:
         for line in lines:
             line["cpu_baseline"] = cpu(w, line["op"])
