@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--suite-iters", type=int, default=50, help="with --suite: timed calls per op")
     ap.add_argument("--suite-no-graphs", action="store_true",
                     help="with --suite: time the decode step eagerly only (no HIP graph capture)")
+    ap.add_argument("--suite-no-fresh", action="store_true",
+                    help="with --suite: time tape ops back to back only (no fresh-payload timing)")
     ap.add_argument("--suite-calibrate", action="store_true",
                     help="with --suite: first copy a 512 MiB tensor (a known-size kernel for counter scaling)")
     return ap.parse_args()
@@ -264,7 +266,7 @@ def main():
                   cpu=None if args.no_cpu_baseline else suite_cpu_baseline,
                   parts=tuple(args.suite_parts) if args.suite_parts else suite.PARTS,
                   configs=args.suite_configs, ops=args.suite_ops, calibrate=args.suite_calibrate,
-                  graphs=not args.suite_no_graphs)
+                  graphs=not args.suite_no_graphs, fresh=not args.suite_no_fresh)
         return
     log("generating cfg4 inputs on the device")
     w = workloads.cfg4(dev, adversarial=args.adversarial)

@@ -92,43 +92,45 @@ def _line(config: str, op: str, us: float, nbytes: int, tokens: int, **extra) ->
 
 
 def tape_lines(w: workloads.Workload, iters: int, cpu: Optional[Callable] = None,
-               ops=("latest_k", "seg_sum", "latest_k_sum")) -> List[dict]:
+               ops=("latest_k", "seg_sum", "latest_k_sum"), fresh: bool = True) -> List[dict]:
     """Each line's us_per_call repeats the call back to back (the inputs it read in its previous
     call may still be in the caches); us_fresh times it after a cache flush and a rewrite of
-    the payload (time_calls_fresh)."""
+    the payload (time_calls_fresh), unless `fresh` is False."""
     B, T, C, D = w.shape
     lines = []
 
     def timed(fn):
         warm = statistics.median(time_calls(fn, iters=iters))
+        if not fresh:
+            return warm, None
         return warm, round(statistics.median(time_calls_fresh(fn, w.payload)), 2)
 
     if "latest_k_sum" in ops:
-        us, fresh = timed(lambda: causal_last_k_and_sum_lookup(w.write, w.payload, w.read,
+        us, us_f = timed(lambda: causal_last_k_and_sum_lookup(w.write, w.payload, w.read,
                                                                address_space=w.address_space, k=w.k))
         lines.append(_line(w.name, "latest_k_sum", us, workloads.algorithmic_bytes_latest_k_sum(w),
                            B * T, shape=[B, T, C, D], k=w.k, A=w.address_space,
                            dtype=str(w.payload.dtype).split(".")[-1],
-                           read="separate" if w.read is not None else "same", us_fresh=fresh))
+                           read="separate" if w.read is not None else "same", us_fresh=us_f))
     if "latest_k" in ops:
-        us, fresh = timed(lambda: causal_last_k_lookup(w.write, w.payload, w.read,
+        us, us_f = timed(lambda: causal_last_k_lookup(w.write, w.payload, w.read,
                                                        address_space=w.address_space, k=w.k))
         lines.append(_line(w.name, "latest_k", us, workloads.algorithmic_bytes_latest_k(w), B * T,
                            shape=[B, T, C, D], k=w.k, A=w.address_space,
                            dtype=str(w.payload.dtype).split(".")[-1],
-                           read="separate" if w.read is not None else "same", us_fresh=fresh))
+                           read="separate" if w.read is not None else "same", us_fresh=us_f))
     if "seg_sum" not in ops:
         if cpu is not None:
             for line in lines:
                 line["cpu_baseline"] = cpu(w, line["op"])
         return lines
-    us, fresh = timed(lambda: causal_sum_lookup(w.write, w.payload, w.read, address_space=w.address_space))
+    us, us_f = timed(lambda: causal_sum_lookup(w.write, w.payload, w.read, address_space=w.address_space))
     N = B * T * C
     esz = w.payload.element_size()
     addr = N * w.write.element_size() * (1 if w.read is None else 2)
     sum_bytes = addr + N * D * esz + N * D * esz + N
     lines.append(_line(w.name, "seg_sum", us, sum_bytes, B * T, shape=[B, T, C, D], A=w.address_space,
-                       us_fresh=fresh))
+                       us_fresh=us_f))
     if cpu is not None:
         for line in lines:
             line["cpu_baseline"] = cpu(w, line["op"])
@@ -386,10 +388,11 @@ TAPE_OPS = ("latest_k", "seg_sum", "latest_k_sum")
 
 def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
         parts=PARTS, configs=None, ops=None, calibrate: bool = False,
-        graphs: bool = True) -> List[dict]:
+        graphs: bool = True, fresh: bool = True) -> List[dict]:
     """Runs the named parts of the suite (all by default) and returns the lines;
-    `configs` and `ops` narrow the tapes part to some configs and ops, and
-    `graphs=False` leaves out the decode part's HIP-graph forms.  With
+    `configs` and `ops` narrow the tapes part to some configs and ops,
+    `graphs=False` leaves out the decode part's HIP-graph forms, and
+    `fresh=False` the tape ops' fresh-payload timing.  With
     `calibrate`, a 512 MiB device copy runs first: a kernel of known traffic
     (512 MiB read, 512 MiB written) by which hardware byte counters are scaled."""
     lines: List[dict] = []
@@ -416,7 +419,7 @@ def run(dev: torch.device, iters: int = 50, cpu: Optional[Callable] = None,
     tapes = [] if "tapes" not in parts else [makers[c] for c in TAPE_CONFIGS if not configs or c in configs]
     for make in tapes:
         w = make()
-        for line in tape_lines(w, iters, cpu, ops=tuple(ops) if ops else TAPE_OPS):
+        for line in tape_lines(w, iters, cpu, ops=tuple(ops) if ops else TAPE_OPS, fresh=fresh):
             print(json.dumps(line), flush=True)
             lines.append(line)
         del w
