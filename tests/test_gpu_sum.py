@@ -136,6 +136,7 @@ CASES = [
     (2, 25, 2, 1, False, False),
     (40, 300, 8, 37, False, False),  # more segments than CUs: 512-thread blocks
     (40, 300, 8, 3, True, True),
+    (8, 512, 4, 2, False, False),  # runs across walkers: every block folds, one iteration a walker
     (3, 5000, 2, 300, False, False),
     (1, 70000, 1, 2, False, False),  # runs spanning hundreds of chunks
     (1, 70000, 1, 3, True, True),
