@@ -1278,16 +1278,14 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   // form): its rows are fetched once, for this tail pass and the final walk.
   // A pass over the whole iteration ends with the tail's sums and flag, since
   // a run start resets them.  (With rings the registers would not hold it.)
+  static_assert(!(SAME && KS == 0) || NB == 1, "one batch an iteration");
   const bool one = SAME && KS == 0 && len == WBI;  // block-uniform
   uint32_t cw1[WBI];
   u32x4 x1[WBI];
   if (one) {
     if (rs < re) {
       fetch(rs, rs, re, std::true_type{}, cw1, x1);
-      if constexpr (NB == 2) fetch(rs + WB, rs, re, std::true_type{}, cw1 + WB, x1 + WB);
       process(cw1, x1, std::integral_constant<int, 0>{}, std::false_type{});
-      if constexpr (NB == 2)
-        process(cw1 + WB, x1 + WB, std::integral_constant<int, 1>{}, std::false_type{});
     }
   } else {
     walk(last >= 0 ? last : rs, re, std::false_type{});
@@ -1402,11 +1400,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
           prs, (__umul24(ring[j], tstride) + v16) | (j < rcnt ? 0u : kCodeNoLoad), 0, 0);
   }
   if (one) {
-    if (rs < re) {
-      process(cw1, x1, std::integral_constant<int, 0>{}, std::true_type{});
-      if constexpr (NB == 2)
-        process(cw1 + WB, x1 + WB, std::integral_constant<int, 1>{}, std::true_type{});
-    }
+    if (rs < re) process(cw1, x1, std::integral_constant<int, 0>{}, std::true_type{});
   } else {
     walk(rs, re, std::true_type{});
   }
