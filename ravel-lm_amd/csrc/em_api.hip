@@ -798,26 +798,6 @@ Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode
   return tp;
 }
 
-const DeviceShape& device_shape(int dev) {
-  static DeviceShape shapes[kMaxDevices];
-  static std::atomic<bool> known[kMaxDevices] = {};
-  static std::mutex mu;
-  static const DeviceShape fallback;
-  if (dev < 0 || dev >= kMaxDevices) return fallback;
-  if (!known[dev].load(std::memory_order_acquire)) {
-    std::lock_guard<std::mutex> lock(mu);
-    if (!known[dev].load(std::memory_order_relaxed)) {
-      int v = 0;
-      if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-          v > 0)
-        shapes[dev].cus = v;
-      if (hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, dev) == hipSuccess && v > 0)
-        shapes[dev].wall_khz = v;
-      known[dev].store(true, std::memory_order_release);
-    }
-  }
-  return shapes[dev];
-}
 
 }  // namespace rem
 

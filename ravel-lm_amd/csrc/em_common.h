@@ -84,18 +84,10 @@ constexpr size_t kStatusBytes = 256;
 // word 1: the bits of the earlier row ranges of a call split by batch rows
 // (each range's first kernel clears word 0)
 constexpr int kStatusSplitWord = 1;
-// words 2-3 of the status area: the merged sum kernel's start gate (a
-// launch sequence number and a count; a scheduling hint, never an error)
-constexpr int kStatusGateWord = 2;
+// words 2-3: unused
 // word 4: the latest-k half's bits while the sum half of a joint call runs
 constexpr int kStatusJointWord = 4;
 
-// Compute units and wall-clock rate (kHz) of a device, queried once.
-struct DeviceShape {
-  int cus = 256;
-  int wall_khz = 100000;
-};
-const DeviceShape& device_shape(int dev);
 
 int bit_width_u64(uint64_t x);
 Tape make_tape(int64_t B, int64_t T, int64_t C, int64_t A, bool masked, int mode);

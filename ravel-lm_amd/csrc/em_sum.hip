@@ -752,27 +752,6 @@ constexpr int kMergedRingOff = kMergedStartOff + kMergedThreads * 4;
 constexpr int kMergedRingBytes = kMergedMaskOff - kMergedRingOff;
 static_assert(kMergedMaskOff + kMergedItems / 2 + 1 <= kMergedUnion, "mask bytes fit");
 
-// Start gate of the merged kernel.  With every block resident at once, all
-// blocks would sort (LDS-bound) together and then walk (HBM-bound) together.
-// Blocks [gate_lo, gate_hi) (the second block of each CU) instead wait until
-// gate_target of the blocks below gate_lo have finished their sort, so one
-// block per CU sorts while the other walks.  The gate word holds the low 16
-// bits of the launch's sequence number (high half, stored by block 0 as the
-// kernel starts) and the count of finished sorts (low half, one atomic add
-// each).  The wait is a scheduling hint only: it ends after gate_ticks of the
-// wall clock whatever the word says, and nothing the kernel computes depends
-// on it.
-__device__ __forceinline__ void gate_wait(const uint32_t* gate, uint32_t tag, uint32_t target,
-                                          uint32_t ticks) {
-  const uint64_t t0 = wall_clock64();
-  for (;;) {
-    const uint32_t v = __hip_atomic_load(gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((v >> 16) == tag && (v & 0xffffu) >= target) return;
-    if (wall_clock64() - t0 >= ticks) return;
-    __builtin_amdgcn_s_sleep(4);
-  }
-}
-
 // One segment's column of a dense [B, T, C] address tensor (2, 4 or 8-byte
 // elements; time t at byte t * stride of base) through a buffer descriptor:
 // each element is read as the two dwords from the aligned dword holding it,
@@ -854,8 +833,7 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     const uint8_t* __restrict__ wmask, int64_t T, int64_t C, int64_t A, int trunc32, int tbits,
     int npass, int G, int64_t nseg, const XIn* __restrict__ payload,
     XIn* __restrict__ out, uint8_t* __restrict__ omask, uint32_t* __restrict__ status,
-    uint32_t* __restrict__ gate, uint32_t tag, uint32_t gate_lo, uint32_t gate_hi,
-    uint32_t gate_target, uint32_t gate_ticks, int kslots, XIn* __restrict__ vout,
+    int kslots, XIn* __restrict__ vout,
     uint8_t* __restrict__ vmask, int32_t* __restrict__ osrc) {
   constexpr int NT = kMergedThreads;
   constexpr int NWV = NT / kWave;
@@ -879,24 +857,12 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
   static_assert(NWV * kRankRadix * sizeof(uint32_t) + kMergedLr * sizeof(uint32_t) <= kMergedUnion,
                 "counters and last-read table share the union");
   const int tid = threadIdx.x, wv = tid / kWave, lane = tid % kWave;
-  if (blockIdx.x == 0 && tid == 0) {
-    *status = 0;  // no waits in this kernel
-    __hip_atomic_store(gate, tag << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  const bool gated = blockIdx.x >= gate_lo && blockIdx.x < gate_hi;
-  const bool signals = blockIdx.x < gate_lo && gate_hi > gate_lo;
+  if (blockIdx.x == 0 && tid == 0) *status = 0;  // no waits in this kernel
   const int64_t seg = xcd_block(blockIdx.x, gridDim.x);
-  if (seg >= nseg) {  // uniform per block
-    if (signals && tid == 0) atomicAdd(gate, 1u);
-    return;
-  }
+  if (seg >= nseg) return;  // uniform per block
   const int64_t b = seg / C, c = seg - (seg / C) * C;
   const int n2 = (int)(2 * T);
   const int tb1 = tbits + 1;
-  if (gated) {
-    if (tid == 0) gate_wait(gate, tag, gate_target, gate_ticks);
-    __syncthreads();
-  }
   // 1. merged keys (straight to LDS) from the segment's address columns;
   // thread tid takes times tid, tid + NT, ...
   if constexpr (SAME) {
@@ -1056,7 +1022,6 @@ __global__ __launch_bounds__(kMergedThreads) __attribute__((amdgpu_waves_per_eu(
     }
   }
   __syncthreads();
-  if (signals && tid == 0) atomicAdd(gate, 1u);  // the LDS-bound part is done
   // 3. the walk: walker w owns items [rs, re), whole batches
   const int NW = NT / G;
   const int w = tid / G, v = tid - (tid / G) * G;
@@ -1469,24 +1434,13 @@ hipError_t seg_sum_merged_t(const AddrIn& wa, const AddrIn* ra, const uint8_t* w
   const int64_t G = D * (int64_t)sizeof(S) / 16;
   const int npass = (tp.abits + 7) / 8;
   const unsigned grid = xcd_grid(tp.nseg(), 1, (int64_t)1 << 31);
-  // the start gate: with two blocks per CU, the second of each CU waits for
-  // three quarters of the first ones' sorts (at most ~200 us)
-  int dev = 0;
-  if (hipError_t e = hipStreamGetDevice(s, &dev)) return e;
-  const DeviceShape& ds = device_shape(dev);
-  const uint32_t lo = (uint32_t)ds.cus, hi = grid < 2u * lo ? grid : 2u * lo;
-  const uint32_t gate_lo = hi > lo ? lo : grid, gate_hi = hi > lo ? hi : grid;
-  const uint32_t target = lo * 3 / 4, ticks = (uint32_t)(ds.wall_khz / 5);
-  static std::atomic<uint32_t> launches{0};
-  const uint32_t tag = (launches.fetch_add(1, std::memory_order_relaxed) + 1u) & 0xffffu;
-  uint32_t* gate = tp.status + kStatusGateWord;
   // reads at the write addresses and no mask: sort the write keys only
   const bool same = !ra && !wmask;
 #define REM_MG(IT, KS, SM, VT)                                                                 \
   segsum_merged_kernel<IT, KS, SM, VT, S, Acc, E, E><<<grid, kMergedThreads, 0, s>>>(         \
       wa.dense, wa.kind, r.dense, r.kind, wmask, tp.T, tp.C, tp.A, tp.trunc32 ? 1 : 0,         \
-      tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, gate,  \
-      tag, gate_lo, gate_hi, target, ticks, k, (S*)vout, vmask, osrc)
+      tp.tbits, npass, (int)G, tp.nseg(), (const S*)payload, (S*)out, omask, tp.status, k,     \
+      (S*)vout, vmask, osrc)
 #define REM_MG_KS(IT, SM)                                                 \
   switch (vout ? merged_ring(k) : 0) {                                   \
     case 0: REM_MG(IT, 0, SM, false); break;                             \
