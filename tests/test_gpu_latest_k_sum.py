@@ -121,6 +121,19 @@ def test_joint_parity(device, case, dtype, D):
                 mask=None if m is None else m.to(device))
 
 
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("k", [3, 8])
+def test_joint_fold_every_row_width(device, G, k):
+    """Runs longer than two walker ranges (two addresses a segment) at every row width of the
+    short-tape kernel: every block folds its walkers' tails and carries their rings."""
+    D = G * 8  # bf16: G 16-byte units a row
+    B, T, C, A = 3, 512, 2, 2
+    g = torch.Generator().manual_seed(G + k)
+    w = torch.randint(0, A, (B, T, C), generator=g)
+    p = torch.randn(B, T, C, D, generator=g).to(torch.bfloat16)
+    check_joint(w.to(device), p.to(device), None, A=A, k=k)
+
+
 @pytest.mark.parametrize("D,dtype", [(5, torch.float32), (3, torch.float16), (1, torch.float64),
                                      (128, torch.bfloat16)])
 def test_joint_row_shapes(device, D, dtype):

@@ -158,6 +158,21 @@ def test_sum_parity(device, case, dtype, D):
               mask=None if m is None else m.to(device))
 
 
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sum_fold_every_row_width(device, G, dtype):
+    """Two addresses a segment make runs longer than two walker ranges, so every block of the
+    short-tape kernel folds its walkers' tails; the fold's groups and the pads between them
+    depend on the 16-byte units of a row, G = 1 .. 64."""
+    D = G * 16 // torch.empty((), dtype=dtype).element_size()
+    B, T, C, A = 3, 512, 2, 2
+    g = torch.Generator().manual_seed(G)
+    w = torch.randint(0, A, (B, T, C), generator=g)
+    p = torch.randn(B, T, C, D, generator=g).to(dtype)
+    print(f"[fold sum] G={G} D={D} {dtype}", flush=True)
+    check_sum(w.to(device), p.to(device), A=A)
+
+
 def test_sum_integer_payloads_are_exact(device):
     """Small integers sum exactly in every dtype: compare bit-for-bit."""
     g = torch.Generator().manual_seed(4)
