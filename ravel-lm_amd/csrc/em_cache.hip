@@ -248,10 +248,13 @@ __global__ __launch_bounds__(256) void prefill_tail_kernel(const U* __restrict__
 constexpr int kPrefillLds = 32 * 1024;  // sorted keys of one segment
 constexpr int kPrefillBatch = 8;        // kept rows in flight per thread (8: 20 us less than 4 at cfg5)
 
-template <typename U, typename V>
+// FD: the segment's T * upr units stay below 2^31, so a unit's row comes from a
+// multiply-high division (a 64-bit division per unit costs more than its row).
+template <typename U, typename V, bool FD>
 __global__ __launch_bounds__(256) void prefill_kept_kernel(
     const U* __restrict__ sorted, const V* __restrict__ payload, int64_t T, int64_t C, int64_t A,
-    int tbits, int64_t k, int64_t upr, V* __restrict__ values, uint8_t* __restrict__ filled) {
+    int tbits, int64_t k, int64_t upr, FastDiv by_upr, V* __restrict__ values,
+    uint8_t* __restrict__ filled) {
   extern __shared__ __align__(16) unsigned char prefill_lds[];
   U* keys = (U*)prefill_lds;
   const int Ti = (int)T;
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(256) void prefill_kept_kernel(
       const int64_t g = g0 + j * 256;
       dst[j] = -1;
       if (g >= units) continue;
-      const int p = (int)(g / upr);
+      const int p = FD ? (int)fdiv((uint32_t)g, by_upr) : (int)(g / upr);
       const int64_t v = g - (int64_t)p * upr;
       const U u = keys[p];
       const U a = u >> tbits;
@@ -400,9 +403,17 @@ hipError_t cache_prefill(const U* sorted, const void* payload, const Tape& tp, i
   const int64_t upr = row_bytes / vb;
   const size_t kept_lds = (size_t)tp.T * sizeof(U);
   if (kept_lds <= (size_t)kPrefillLds) {
+    const bool fd = tp.T * upr < ((int64_t)1 << 31);
+    const FastDiv by_upr = make_fastdiv(fd ? (uint32_t)upr : 1u);
 #define REM_PREFILL(VT)                                                                          \
-  prefill_kept_kernel<U, VT><<<(unsigned)BC, 256, kept_lds, s>>>(                                \
-      sorted, (const VT*)payload, tp.T, tp.C, tp.A, tp.tbits, k, upr, (VT*)values, filled)
+  if (fd)                                                                                        \
+    prefill_kept_kernel<U, VT, true><<<(unsigned)BC, 256, kept_lds, s>>>(                        \
+        sorted, (const VT*)payload, tp.T, tp.C, tp.A, tp.tbits, k, upr, by_upr, (VT*)values,     \
+        filled);                                                                                 \
+  else                                                                                           \
+    prefill_kept_kernel<U, VT, false><<<(unsigned)BC, 256, kept_lds, s>>>(                       \
+        sorted, (const VT*)payload, tp.T, tp.C, tp.A, tp.tbits, k, upr, by_upr, (VT*)values,     \
+        filled)
     switch (vb) {
       case 16: REM_PREFILL(u32x4); break;
       case 8: REM_PREFILL(u32x2); break;
