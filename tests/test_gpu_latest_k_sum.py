@@ -218,6 +218,43 @@ def test_joint_split_ranges(device):
             assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("offs", [(1, 3), (5, 5), (0, 7)])
+def test_joint_walker_masks_at_byte_offsets(device, offs):
+    """The long-tape joint form (reads = writes, no mask, k = 1) writes the sum
+    mask at random records and copies it into the latest-1 mask: through the C
+    entry point, masks that start at any byte offset (alike or unlike modulo 16,
+    so the copy takes its byte path or its head, 16-byte body and tail) equal
+    the aligned call's, and the bytes around them stay untouched."""
+    lib = nat.library()
+    g = torch.Generator().manual_seed(11)
+    B, T, C, D, A = 2, 6000, 3, 64, 700  # T > 4096: the sorted walker path
+    w = torch.randint(0, A, (B, T, C), generator=g).to(device)
+    p = torch.randn(B, T, C, D, generator=g).to(device, torch.bfloat16)
+    want = joint_sources(w, p, None, A, 1, None)
+    n = B * T * C
+    vbuf = torch.full((n + 32,), 0xA5, dtype=torch.uint8, device=device)
+    sbuf = torch.full((n + 32,), 0x5A, dtype=torch.uint8, device=device)
+    o1, o2 = offs
+    values = p.new_empty(B, T, C, 1, D)
+    out = p.new_empty(B, T, C, D)
+    code = nat.payload_code(p.dtype)
+    nbytes = lib.ravel_em_latest_k_sum_workspace(B, T, C, D, A, 1, 0, 0, 0, code)
+    ws = nat.workspace(nbytes, device)
+    print(f"[joint masks] offsets {offs}", flush=True)
+    nat.check(lib.ravel_em_latest_k_sum_fwd(
+        nat.ptr(w), None, nat.addr_code(w.dtype), None, nat.ptr(p), code, B, T, C, D, A, 1,
+        nat.ptr(values), vbuf.data_ptr() + o1, None, nat.ptr(out), sbuf.data_ptr() + o2,
+        nat.ptr(ws), ws.numel(), nat.stream_of(p)))
+    nat.after_call(ws)
+    torch.cuda.synchronize()
+    assert torch.equal(values, want[0]) and torch.equal(out, want[3])
+    assert torch.equal(vbuf[o1:o1 + n].bool(), want[1].reshape(-1))
+    assert torch.equal(sbuf[o2:o2 + n].bool(), want[4].reshape(-1))
+    assert torch.equal(vbuf[o1:o1 + n], sbuf[o2:o2 + n])  # 0/1 bytes, the same in both
+    assert bool((vbuf[:o1] == 0xA5).all()) and bool((vbuf[o1 + n:] == 0xA5).all())
+    assert bool((sbuf[:o2] == 0x5A).all()) and bool((sbuf[o2 + n:] == 0x5A).all())
+
+
 def test_joint_produced_addresses(device):
     """LayerAddresses: addresses produced in the call give the tensor call's results."""
     g = torch.Generator().manual_seed(3)
