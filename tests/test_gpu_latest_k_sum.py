@@ -135,9 +135,11 @@ def test_joint_fold_every_row_width(device, G, k):
 
 
 @pytest.mark.parametrize("D,dtype", [(5, torch.float32), (3, torch.float16), (1, torch.float64),
-                                     (128, torch.bfloat16)])
+                                     (128, torch.bfloat16), (64, torch.float16),
+                                     (8, torch.float64)])
 def test_joint_row_shapes(device, D, dtype):
-    """Rows that are not whole 16-byte units (the pair) and wide rows."""
+    """Rows that are not whole 16-byte units (the pair), wide rows, and fp16 and
+    fp64 rows of whole units (the long tape's walker writes their values)."""
     g = torch.Generator().manual_seed(D)
     for (B, T, C, A, k) in [(2, 300, 3, 17, 3), (2, 6000, 2, 40, 1)]:
         w = torch.randint(0, A, (B, T, C), generator=g)
